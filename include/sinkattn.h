@@ -1,0 +1,161 @@
+/*
+ * libsinkattn — MI355X (gfx950) kernels for SinkAttention's sparse-attention hot path.
+ *
+ * C ABI: plain device pointers, int64 shapes, element strides, a hipStream_t passed as
+ * void*.  Every entry point returns an int status:
+ *     0            success (work is enqueued on `stream`, nothing is synchronised)
+ *    <0            invalid argument (nothing was enqueued); see sinkattn_last_error()
+ *    >0            a hipError_t from a launch
+ * No C++ exception crosses this boundary and no entry point allocates device memory:
+ * outputs and workspaces are supplied by the caller (sizes from the *_bytes queries).
+ * Functions are stateless and reentrant; all work is stream-ordered.
+ *
+ * Tensor conventions.  A "BHSD" operand is addressed as
+ *     base[b*s[0] + h*s[1] + n*s[2] + d*s[3]]   with s[3] == 1,
+ * so both contiguous [B,H,N,D] tensors and [B,N,H,D] memory viewed as [B,H,N,D]
+ * (what the reference's varlen call produces) are accepted without copies.
+ * Vector loads need the base 16-byte aligned and s[0..2] multiples of 8 elements.
+ *
+ * The reference (bb-2020-bb/sinkattn) is Python; the citations below name the Python
+ * function each entry point replaces.
+ */
+#ifndef SINKATTN_H_
+#define SINKATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of Q/K/V/O. */
+enum sinkattn_dtype { SINKATTN_BF16 = 0, SINKATTN_F16 = 1, SINKATTN_F32 = 2 };
+
+/* Message for the last non-zero status returned on the calling thread ("" if none). */
+const char* sinkattn_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int sinkattn_abi_version(void);
+
+/* ------------------------------------------------------------------------------------
+ * Block-sparse plan: bool block mask -> per-(b,h,q-block) ascending key-block lists.
+ *
+ * Replaces the mask hand-off of `_block_sparse_attn` -> `block_sparse_attn_func(...,
+ * base_blockmask=block_mask.contiguous(), ...)` (sinkattention/sparse_attention.py:743,762):
+ * the external kernel consumed the bool mask directly; here it is turned once into
+ *   counts[B*H*nqb]          number of listed key blocks per row,
+ *   idx[B*H*nqb*nkb]         the listed key blocks of row r in idx[r*nkb .. r*nkb+counts[r]),
+ *   order[B*H*nqb]           rows sorted by descending count (longest-first launch order).
+ * `mask` is uint8/bool [B,H,nqb,nkb] with element strides mask_strides[4].
+ * ---------------------------------------------------------------------------------- */
+int sinkattn_block_sparse_plan(const uint8_t* mask, const int64_t mask_strides[4],
+                               int64_t B, int64_t H, int64_t nqb, int64_t nkb,
+                               int32_t* counts, int32_t* idx, int32_t* order,
+                               void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Block-sparse flash-attention forward, 128x128 tiles.
+ *
+ * Replaces `block_sparse_attn_func` as called by `_block_sparse_attn`
+ * (sinkattention/sparse_attention.py:710-776): for every query row of q-block qb the
+ * keys of the listed key blocks (and only keys < Nk) are attended:
+ *     out = softmax(scale * Q K^T + M) V,   lse = log(sum(exp(scale * Q K^T + M)))
+ * with M = 0 on listed tiles and -inf elsewhere.  q/k/v/out are BHSD-addressed (see
+ * above), dtype one of sinkattn_dtype (f32 operands are rounded to bf16 for the matrix
+ * cores; accumulation and softmax are fp32).  lse is fp32 [B,H,Nq] contiguous, or NULL.
+ * A row with no listed key block gets out = 0 and lse = +inf.
+ * counts/idx/order come from sinkattn_block_sparse_plan (order may be NULL).
+ * D must be 64 or 128.
+ * ---------------------------------------------------------------------------------- */
+int sinkattn_block_sparse_fwd(const void* q, const void* k, const void* v, int dtype,
+                              int64_t B, int64_t H, int64_t Nq, int64_t Nk, int64_t D,
+                              const int64_t q_strides[4], const int64_t k_strides[4],
+                              const int64_t v_strides[4],
+                              void* out, const int64_t out_strides[4], float* lse,
+                              const int32_t* counts, const int32_t* idx,
+                              const int32_t* order, int64_t nqb, int64_t nkb,
+                              float softmax_scale, void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Exact block-mass pooling ("exact" pooling mode).
+ *
+ * Replaces `_compute_exact_block_mass_scores` (sinkattention/sparse_attention.py:145-227):
+ *     P = softmax_rows(scale * Q K^T)                  (fp32, over all Nk keys)
+ *     out[b,h,qb,kb] = mean over the rows r of q-block qb of  sum_{j in kb} P[r,j]
+ * out is fp32 [B,H,nqb,nkb] contiguous, nqb = ceil(Nq/block), nkb = ceil(Nk/block).
+ * bf16/f16 inputs use the matrix cores (exact products, fp32 sums); f32 inputs use the
+ * fp32 matrix path.  block_size must be 128.  Requires nkb <= 256 for bf16/f16
+ * (128-row work-groups) and nkb <= 256 for f32 (64-row work-groups).
+ * ---------------------------------------------------------------------------------- */
+int sinkattn_block_mass_pool(const void* q, const void* k, int dtype,
+                             int64_t B, int64_t H, int64_t Nq, int64_t Nk, int64_t D,
+                             const int64_t q_strides[4], const int64_t k_strides[4],
+                             int64_t block_size, float scale, float* out,
+                             void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Row-normalised max-pool map ("triton" pooling mode).
+ *
+ * Replaces `attn_with_pooling` (sinkattention/pooling_kernel.py:194-248) minus its
+ * all-zero `o` output and its [B,H,N,nd] scratch:
+ *     R[r,kb]  = q.dtype( max_{j in kb} (q_r . k_j) * sm_scale * log2(e) )
+ *     m_r      = max over kb of the unrounded block maxima
+ *     Po[qb,kb]= q.dtype( max_{r in qb} exp2(R[r,kb] - m_r) )
+ *     Po      /= q.dtype( sum_kb Po[qb,kb] )           (row normalisation in q.dtype)
+ * Po is written in q.dtype (bf16 or f16) as [B,H,nd,nd] contiguous.  kv head of query
+ * head h is h / (H / Hk).  causal restricts row qb to kb <= qb and adds -1e6 to the
+ * raw scores above the diagonal of the diagonal tile, as the reference does.  Keys and
+ * rows >= N are excluded (the reference leaves ragged N undefined).  block_size = 128.
+ * ---------------------------------------------------------------------------------- */
+int sinkattn_max_pool(const void* q, const void* k, int dtype,
+                      int64_t B, int64_t H, int64_t Hk, int64_t N, int64_t D,
+                      const int64_t q_strides[4], const int64_t k_strides[4],
+                      int64_t block_size, float sm_scale, int causal, void* po,
+                      void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Mean-pooled block scores ("mean" pooling mode).
+ *
+ * Replaces `_compute_pooled_qk_block_scores`'s fallback branch with `_mean_pool_sequence`
+ * / `_pad_to_multiple` (sinkattention/sparse_attention.py:79-94,138-142):
+ *     Qp = mean over each block of rows of Q padded to a multiple of block by repeating
+ *          its last row (likewise Kp);   out = softmax_rows(scale * Qp Kp^T)
+ * out fp32 [B,H,nqb,nkb] contiguous.  workspace: sinkattn_mean_pool_workspace_bytes().
+ * ---------------------------------------------------------------------------------- */
+size_t sinkattn_mean_pool_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nk,
+                                          int64_t D, int64_t block_size);
+int sinkattn_mean_pool_scores(const void* q, const void* k, int dtype,
+                              int64_t B, int64_t H, int64_t Nq, int64_t Nk, int64_t D,
+                              const int64_t q_strides[4], const int64_t k_strides[4],
+                              int64_t block_size, float scale, void* workspace,
+                              float* out, void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Direct-mean coverage mask.
+ *
+ * Replaces `_build_direct_mean_coverage_mask` + `_build_offline_required_mask`
+ * (sinkattention/sparse_attention.py:241-376), bit-exact with the reference's CPU torch
+ * arithmetic.  scores: fp32 [H,nq,nk] contiguous.  Required blocks: every row's first
+ * `req_k` columns and the first `req_q` rows entirely (both 0 when the reference's
+ * required mask is None).  mode 0 = "joint" branch, 1 = "video_residual" branch with
+ * `text_blocks` leading text blocks.  coverage is the already-clamped fp32 value.
+ * Outputs: mask uint8 [H,nq,nk]; counts int32 [H,nq]; idx int32 [H,nq,nk] (ascending
+ * key blocks of each row, counts[r] valid entries).  counts/idx may be NULL.
+ * The reference's empty-row fallback is reproduced as written: if any row of the whole
+ * tensor ends up empty, every row r gets mask[r, top1(r)] = (row r was empty), which
+ * also clears that bit in non-empty rows.  workspace: *_workspace_bytes(H, nq).
+ * nk <= 1024.
+ * ---------------------------------------------------------------------------------- */
+size_t sinkattn_coverage_mask_workspace_bytes(int64_t H, int64_t nq);
+int sinkattn_coverage_mask(const float* scores, int64_t H, int64_t nq, int64_t nk,
+                           float coverage, int keep_diagonal, int64_t req_q,
+                           int64_t req_k, int mode, int64_t text_blocks,
+                           uint8_t* mask, int32_t* counts, int32_t* idx,
+                           void* workspace, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SINKATTN_H_ */

@@ -1,0 +1,30 @@
+"""TEST INFRASTRUCTURE ONLY: CPU parity oracle for the sparse-attention hot path.
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg may import
+this package, and only as the checker (or the timed CPU baseline), never as the product
+path.  The product (``sinkattn_amd``) never imports it.
+
+Contents
+--------
+torch_ref   CPU torch restatements of the reference functions, each citing the
+            reference file:line it follows (exact block mass, max-pool closed form,
+            mean-pooled scores, coverage mask, required mask, dense masked softmax
+            attention with LSE, LSE mixing).
+c_ref       ctypes loader of oracle/_build/liboracle.so: the plain-C coverage-mask
+            restatement (ATen fp32 sum order, fp64 cumsum, libstdc++ std::sort
+            emulation) and the real libstdc++ std::sort.
+
+How each function is pinned (tests/test_oracle_*.py):
+  exact block mass     fp64 brute force on small shapes; closed forms (rows sum to 1,
+                       Q = 0 gives |kb|/N, a dominant sink key gives block 0 -> 1)
+  max-pool             fp64 evaluation of the formula, row normalisation invariant
+  mean-pooled scores   closed form (softmax of pooled dot products, padding rule)
+  coverage mask        C model vs torch on this machine (sum order, cumsum, sort
+                       permutation incl. ties), emulated vs real std::sort, brute-force
+                       minimal-k definition on small rows, invariants and special cases
+  dense attention      SDPA on a full mask, block-local attention on a diagonal mask,
+                       logsumexp identity
+Parity unpinned: the bf16 bit pattern of the reference Triton max-pool kernel
+(``attn_with_pooling``) beyond "within bf16 rounding", and its ragged-N behaviour
+(undefined in the reference).
+"""

@@ -1,0 +1,248 @@
+// extern "C" entry points of libsinkattn (declared in include/sinkattn.h): argument
+// validation, then a stream-ordered launch.  Nothing here allocates device memory.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/sinkattn.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return -1;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return 0;
+  g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+  return (int)e;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool valid_dtype(int dt) { return dt == SINKATTN_BF16 || dt == SINKATTN_F16 || dt == SINKATTN_F32; }
+
+// BHSD operand: innermost stride 1, 16-byte aligned base, outer strides multiples of 8.
+int check_operand(const char* name, const void* p, const int64_t* s) {
+  if (p == nullptr) return fail("%s: null pointer", name);
+  if (s == nullptr) return fail("%s: null strides", name);
+  if (s[3] != 1) return fail("%s: innermost stride must be 1 (got %lld)", name, (long long)s[3]);
+  if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return fail("%s: base must be 16-byte aligned", name);
+  for (int i = 0; i < 3; ++i)
+    if (s[i] % 8 != 0 || s[i] < 0)
+      return fail("%s: stride[%d]=%lld must be a non-negative multiple of 8 elements", name, i,
+                  (long long)s[i]);
+  return 0;
+}
+
+const int64_t kMaxInt = 0x7fffffffLL;
+
+}  // namespace
+
+extern "C" {
+
+const char* sinkattn_last_error(void) { return g_last_error.c_str(); }
+
+int sinkattn_abi_version(void) { return 1; }
+
+int sinkattn_block_sparse_plan(const uint8_t* mask, const int64_t mask_strides[4], int64_t B,
+                               int64_t H, int64_t nqb, int64_t nkb, int32_t* counts,
+                               int32_t* idx, int32_t* order, void* stream) {
+  if (B < 0 || H < 0 || nqb < 0 || nkb < 0) return fail("plan: negative size");
+  const int64_t rows = B * H * nqb;
+  if (rows > kMaxInt || nkb > 8192) return fail("plan: too many rows or key blocks (nkb <= 8192)");
+  if (rows == 0) return 0;
+  if (mask == nullptr || mask_strides == nullptr || counts == nullptr || idx == nullptr)
+    return fail("plan: null pointer");
+  sa::PlanArgs a{};
+  a.mask = mask;
+  for (int i = 0; i < 4; ++i) a.ms[i] = mask_strides[i];
+  a.H = (int)H;
+  a.nqb = (int)nqb;
+  a.nkb = (int)nkb;
+  a.rows = (int)rows;
+  a.counts = counts;
+  a.idx = idx;
+  a.order = order;
+  return hip_status(sa::launch_block_sparse_plan(a, (hipStream_t)stream), "plan launch");
+}
+
+int sinkattn_block_sparse_fwd(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                              int64_t H, int64_t Nq, int64_t Nk, int64_t D,
+                              const int64_t q_strides[4], const int64_t k_strides[4],
+                              const int64_t v_strides[4], void* out,
+                              const int64_t out_strides[4], float* lse, const int32_t* counts,
+                              const int32_t* idx, const int32_t* order, int64_t nqb, int64_t nkb,
+                              float softmax_scale, void* stream) {
+  if (!valid_dtype(dtype)) return fail("fwd: unsupported dtype %d", dtype);
+  if (D != 64 && D != 128) return fail("fwd: head dim %lld not supported (64 or 128)", (long long)D);
+  if (B < 0 || H < 0 || Nq < 0 || Nk < 0) return fail("fwd: negative size");
+  if (nqb != cdiv(Nq, 128) || nkb != cdiv(Nk, 128))
+    return fail("fwd: plan is [%lld,%lld] blocks, expected [%lld,%lld]", (long long)nqb,
+                (long long)nkb, (long long)cdiv(Nq, 128), (long long)cdiv(Nk, 128));
+  if (B * H * nqb > kMaxInt || Nq > kMaxInt || Nk > kMaxInt) return fail("fwd: sizes exceed int32");
+  if (B * H * nqb == 0) return 0;
+  int rc;
+  if ((rc = check_operand("q", q, q_strides)) != 0) return rc;
+  if ((rc = check_operand("k", k, k_strides)) != 0) return rc;
+  if ((rc = check_operand("v", v, v_strides)) != 0) return rc;
+  if ((rc = check_operand("out", out, out_strides)) != 0) return rc;
+  if (counts == nullptr || idx == nullptr) return fail("fwd: null plan");
+  sa::FwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.lse = lse;
+  for (int i = 0; i < 4; ++i) {
+    a.qs[i] = q_strides[i];
+    a.ks[i] = k_strides[i];
+    a.vs[i] = v_strides[i];
+    a.os[i] = out_strides[i];
+  }
+  a.counts = counts;
+  a.idx = idx;
+  a.order = order;
+  a.B = (int)B;
+  a.H = (int)H;
+  a.Nq = (int)Nq;
+  a.Nk = (int)Nk;
+  a.nqb = (int)nqb;
+  a.nkb = (int)nkb;
+  a.scale = softmax_scale;
+  return hip_status(sa::launch_block_sparse_fwd(a, dtype, (int)D, (hipStream_t)stream), "fwd launch");
+}
+
+static int fill_pool_args(sa::PoolArgs& a, const char* who, const void* q, const void* k, int dtype,
+                          int64_t B, int64_t H, int64_t Hk, int64_t Nq, int64_t Nk, int64_t D,
+                          const int64_t* qs, const int64_t* ks, int64_t block_size) {
+  if (!valid_dtype(dtype)) return fail("%s: unsupported dtype %d", who, dtype);
+  if (block_size != 128) return fail("%s: block_size %lld not supported (128)", who, (long long)block_size);
+  if (D != 128) return fail("%s: head dim %lld not supported (128)", who, (long long)D);
+  if (B < 0 || H < 0 || Hk <= 0 || Nq < 0 || Nk < 0) return fail("%s: bad size", who);
+  if (H % Hk != 0) return fail("%s: query heads %lld not a multiple of kv heads %lld", who, (long long)H, (long long)Hk);
+  if (Nq > kMaxInt || Nk > kMaxInt || B * H * cdiv(Nq, 128) > kMaxInt) return fail("%s: sizes exceed int32", who);
+  int rc;
+  if (B * H * Nq > 0) {
+    if ((rc = check_operand("q", q, qs)) != 0) return rc;
+    if ((rc = check_operand("k", k, ks)) != 0) return rc;
+  }
+  a.q = q;
+  a.k = k;
+  for (int i = 0; i < 4; ++i) {
+    a.qs[i] = qs[i];
+    a.ks[i] = ks[i];
+  }
+  a.B = (int)B;
+  a.H = (int)H;
+  a.Hk = (int)Hk;
+  a.Nq = (int)Nq;
+  a.Nk = (int)Nk;
+  a.nqb = (int)cdiv(Nq, block_size);
+  a.nkb = (int)cdiv(Nk, block_size);
+  return 0;
+}
+
+int sinkattn_block_mass_pool(const void* q, const void* k, int dtype, int64_t B, int64_t H,
+                             int64_t Nq, int64_t Nk, int64_t D, const int64_t q_strides[4],
+                             const int64_t k_strides[4], int64_t block_size, float scale,
+                             float* out, void* stream) {
+  sa::PoolArgs a{};
+  int rc = fill_pool_args(a, "block_mass_pool", q, k, dtype, B, H, H, Nq, Nk, D, q_strides,
+                          k_strides, block_size);
+  if (rc != 0) return rc;
+  if (Nk == 0) return fail("block_mass_pool: no keys");
+  if (a.nkb > 256) return fail("block_mass_pool: %d key blocks exceed the supported 256", a.nkb);
+  if (out == nullptr) return fail("block_mass_pool: null output");
+  a.scale = scale;
+  a.out = out;
+  return hip_status(sa::launch_block_mass_pool(a, dtype, (int)D, (hipStream_t)stream), "pool launch");
+}
+
+int sinkattn_max_pool(const void* q, const void* k, int dtype, int64_t B, int64_t H, int64_t Hk,
+                      int64_t N, int64_t D, const int64_t q_strides[4], const int64_t k_strides[4],
+                      int64_t block_size, float sm_scale, int causal, void* po, void* stream) {
+  sa::PoolArgs a{};
+  if (dtype == SINKATTN_F32) return fail("max_pool: q.dtype must be bf16 or f16");
+  int rc = fill_pool_args(a, "max_pool", q, k, dtype, B, H, Hk, N, N, D, q_strides, k_strides,
+                          block_size);
+  if (rc != 0) return rc;
+  if (a.nkb > 256) return fail("max_pool: %d key blocks exceed the supported 256", a.nkb);
+  if (po == nullptr) return fail("max_pool: null output");
+  a.scale = sm_scale;
+  a.causal = causal ? 1 : 0;
+  a.out = po;
+  return hip_status(sa::launch_max_pool(a, dtype, (int)D, (hipStream_t)stream), "max_pool launch");
+}
+
+size_t sinkattn_mean_pool_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nk, int64_t D,
+                                          int64_t block_size) {
+  if (block_size <= 0) return 0;
+  return (size_t)(B * H * (cdiv(Nq, block_size) + cdiv(Nk, block_size)) * D) * sizeof(float);
+}
+
+int sinkattn_mean_pool_scores(const void* q, const void* k, int dtype, int64_t B, int64_t H,
+                              int64_t Nq, int64_t Nk, int64_t D, const int64_t q_strides[4],
+                              const int64_t k_strides[4], int64_t block_size, float scale,
+                              void* workspace, float* out, void* stream) {
+  sa::PoolArgs a{};
+  int rc = fill_pool_args(a, "mean_pool", q, k, dtype, B, H, H, Nq, Nk, D, q_strides, k_strides,
+                          block_size);
+  if (rc != 0) return rc;
+  if (Nq == 0 || Nk == 0) return fail("mean_pool: empty sequence");
+  if (workspace == nullptr || out == nullptr) return fail("mean_pool: null workspace or output");
+  a.scale = scale;
+  a.out = out;
+  a.ws = reinterpret_cast<float*>(workspace);
+  return hip_status(sa::launch_mean_pool(a, dtype, (int)D, (hipStream_t)stream), "mean_pool launch");
+}
+
+size_t sinkattn_coverage_mask_workspace_bytes(int64_t H, int64_t nq) {
+  const int64_t rows = H * nq > 0 ? H * nq : 0;
+  return (size_t)(((rows * 4 + 255) / 256) * 256 + ((rows + 255) / 256) * 256);
+}
+
+int sinkattn_coverage_mask(const float* scores, int64_t H, int64_t nq, int64_t nk, float coverage,
+                           int keep_diagonal, int64_t req_q, int64_t req_k, int mode,
+                           int64_t text_blocks, uint8_t* mask, int32_t* counts, int32_t* idx,
+                           void* workspace, void* stream) {
+  if (H < 0 || nq < 0 || nk < 0) return fail("coverage_mask: negative size");
+  if (nk > 1024) return fail("coverage_mask: %lld key blocks exceed the supported 1024", (long long)nk);
+  if (H * nq > kMaxInt) return fail("coverage_mask: too many rows");
+  if (mode != 0 && mode != 1) return fail("coverage_mask: mode must be 0 (joint) or 1 (video_residual)");
+  if (req_q < 0 || req_k < 0 || text_blocks < 0) return fail("coverage_mask: negative block count");
+  if (H * nq * nk == 0) return 0;
+  if (scores == nullptr || mask == nullptr || workspace == nullptr)
+    return fail("coverage_mask: null pointer");
+  sa::MaskArgs a{};
+  a.scores = scores;
+  a.H = (int)H;
+  a.nq = (int)nq;
+  a.nk = (int)nk;
+  a.coverage = coverage;
+  a.keep_diagonal = keep_diagonal ? 1 : 0;
+  a.req_q = (int)(req_q < nq ? req_q : nq);
+  a.req_k = (int)(req_k < nk ? req_k : nk);
+  a.mode = mode;
+  a.text_blocks = (int)text_blocks;
+  a.mask = mask;
+  a.counts = counts;
+  a.idx = idx;
+  a.ws_top1 = reinterpret_cast<int32_t*>(workspace);
+  a.ws_flags = reinterpret_cast<uint8_t*>(workspace) + ((H * nq * 4 + 255) / 256) * 256;
+  return hip_status(sa::launch_coverage_mask(a, (hipStream_t)stream), "coverage_mask launch");
+}
+
+}  // extern "C"

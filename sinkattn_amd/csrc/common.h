@@ -1,0 +1,141 @@
+// Shared device helpers for the gfx950 kernels of libsinkattn.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+enum DType { kBF16 = 0, kF16 = 1, kF32 = 2 };
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+__device__ __forceinline__ float pos_inf() { return __builtin_inff(); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// fp32 -> 16-bit float bits, round to nearest even (hardware v_cvt_pk_bf16_f32 / cvt_f16).
+template <int CT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2<kBF16>(float lo, float hi) {
+  __bf16 a = (__bf16)lo, b = (__bf16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<kF16>(float lo, float hi) {
+  _Float16 a = (_Float16)lo, b = (_Float16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// 32x32x16 MFMA, A/B as 8 packed 16-bit values in a u32x4.
+template <int CT>
+__device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c);
+template <>
+__device__ __forceinline__ f32x16 mfma32x32x16<kBF16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma32x32x16<kF16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Cross-lane exchange with lane ^ 32 (the two halves of a 32x32 MFMA column).
+__device__ __forceinline__ float xor32(float x) {
+  return __shfl_xor(x, 32, 64);
+}
+
+// Load 8 consecutive elements of type IT at p (16-byte aligned for 16-bit types,
+// 32-byte aligned for f32) and return them as 8 packed 16-bit values of type CT.
+template <int IT, int CT>
+__device__ __forceinline__ u32x4 load8(const void* p);
+template <>
+__device__ __forceinline__ u32x4 load8<kBF16, kBF16>(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+template <>
+__device__ __forceinline__ u32x4 load8<kF16, kF16>(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+template <>
+__device__ __forceinline__ u32x4 load8<kF32, kBF16>(const void* p) {
+  const f32x4* f = reinterpret_cast<const f32x4*>(p);
+  f32x4 a = f[0], b = f[1];
+  u32x4 r;
+  r[0] = pack2<kBF16>(a[0], a[1]);
+  r[1] = pack2<kBF16>(a[2], a[3]);
+  r[2] = pack2<kBF16>(b[0], b[1]);
+  r[3] = pack2<kBF16>(b[2], b[3]);
+  return r;
+}
+
+// Load 2 consecutive elements as one packed pair of CT values.
+template <int IT, int CT>
+__device__ __forceinline__ uint32_t load2(const void* p);
+template <>
+__device__ __forceinline__ uint32_t load2<kBF16, kBF16>(const void* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
+}
+template <>
+__device__ __forceinline__ uint32_t load2<kF16, kF16>(const void* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
+}
+template <>
+__device__ __forceinline__ uint32_t load2<kF32, kBF16>(const void* p) {
+  f32x2 a = *reinterpret_cast<const f32x2*>(p);
+  return pack2<kBF16>(a[0], a[1]);
+}
+
+template <int IT>
+struct ElemSize;
+template <>
+struct ElemSize<kBF16> { static constexpr int value = 2; };
+template <>
+struct ElemSize<kF16> { static constexpr int value = 2; };
+template <>
+struct ElemSize<kF32> { static constexpr int value = 4; };
+
+// Store 4 fp32 values as 4 consecutive elements of type IT.
+template <int IT>
+__device__ __forceinline__ void store4(void* p, float a, float b, float c, float d);
+template <>
+__device__ __forceinline__ void store4<kBF16>(void* p, float a, float b, float c, float d) {
+  u32x2 v;
+  v[0] = pack2<kBF16>(a, b);
+  v[1] = pack2<kBF16>(c, d);
+  *reinterpret_cast<u32x2*>(p) = v;
+}
+template <>
+__device__ __forceinline__ void store4<kF16>(void* p, float a, float b, float c, float d) {
+  u32x2 v;
+  v[0] = pack2<kF16>(a, b);
+  v[1] = pack2<kF16>(c, d);
+  *reinterpret_cast<u32x2*>(p) = v;
+}
+template <>
+__device__ __forceinline__ void store4<kF32>(void* p, float a, float b, float c, float d) {
+  f32x4 v;
+  v[0] = a; v[1] = b; v[2] = c; v[3] = d;
+  *reinterpret_cast<f32x4*>(p) = v;
+}
+
+}  // namespace sa

@@ -1,0 +1,425 @@
+// Block-score ("pooling") kernels for gfx950.
+//
+// block_mass_pool: the reference's exact mode, `_compute_exact_block_mass_scores`
+//   (sinkattention/sparse_attention.py:145-227), in one pass over K with no N x N
+//   intermediate.  A work-group owns one q-block (32*NW rows).  For every key tile it
+//   computes S^T with the matrix cores, turns each row's scores into exp2 terms relative
+//   to a per-row reference maximum, and keeps the per-(row, key-block) sums in LDS.  The
+//   reference maximum is only moved when a tile's maximum exceeds it by more than
+//   kRescaleMargin (log2 units); then the row's earlier sums are rescaled.  At the end
+//   every row is normalised by its own total and the rows are averaged per key block.
+//
+// max_pool: `attn_with_pooling` (sinkattention/pooling_kernel.py:11-248) without the
+//   [B,H,N,nd] scratch: the per-(row, key-block) maxima live in LDS.
+//
+// mean_pool: `_compute_pooled_qk_block_scores`' mean branch
+//   (sinkattention/sparse_attention.py:79-94,138-142).
+
+#include "common.h"
+#include "kernels.h"
+#include "tile.h"
+
+namespace sa {
+
+constexpr float kRescaleMargin = 8.f;
+
+// ------------------------------------------------------------------------------------
+// Exact block mass, 16-bit inputs (exact products on the bf16/f16 matrix cores).
+// ------------------------------------------------------------------------------------
+template <int IT, int CT, int NKBMAX>
+__global__ __launch_bounds__(256) void block_mass_kernel(PoolArgs a) {
+  constexpr int D = 128;
+  constexpr int ES = ElemSize<IT>::value;
+  constexpr int KC = D / 8;
+  __shared__ u32x4 lds_k[128 * KC];           // 32 KB; reused for 1/L at the end
+  __shared__ float sums[128 * NKBMAX];        // per-(row, key-block) partial mass
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int qb = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int nkb = a.nkb;
+
+  const char* qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * ES;
+  const char* kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)h * a.ks[1]) * ES;
+
+  const int r = wave * 32 + l32;  // row within the q-block
+  const int qrow = qb * 128 + r;
+  u32x4 qf[D / 16];
+  load_q_operand<IT, CT, D>(qf, qbase, a.qs[2], qrow, a.Nq, hl);
+
+  const int prow = k_row_perm(l32);
+  const int fk = k_swz(prow);
+  const float c = a.scale * kLog2e;
+  float m_ref = neg_inf();
+  float* my = sums + r * NKBMAX;
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int key0 = kb * 128;
+    __syncthreads();
+    stage_k_tile<IT, CT, D, 256>(lds_k, kbase, a.ks[2], key0, a.Nk, tid);
+    __syncthreads();
+    f32x16 s[4];
+    qk_tile<CT, D>(lds_k, qf, prow, fk, hl, s);
+    if (key0 + 128 > a.Nk) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (key0 + t * 32 + tile_key(hl, j) >= a.Nk) s[t][j] = neg_inf();
+    }
+    float mx = neg_inf();
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
+    mx = fmaxf(mx, xor32(mx)) * c;
+    if (mx > m_ref + kRescaleMargin) {
+      // Move the reference maximum; rescale this row's earlier sums (the two lanes of
+      // the row split the entries by parity).
+      const float f = fast_exp2(m_ref - mx);
+      for (int j = hl; j < kb; j += 2) my[j] *= f;
+      m_ref = mx;
+    }
+    float ps = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) ps += fast_exp2(__builtin_fmaf(s[t][j], c, -m_ref));
+    ps += xor32(ps);
+    if (hl == 0) my[kb] = ps;
+  }
+  __syncthreads();
+
+  // Row totals in the (now free) K-tile storage.
+  float* row_tot = reinterpret_cast<float*>(lds_k);
+  {
+    float tot = 0.f;
+    for (int j = hl; j < nkb; j += 2) tot += my[j];
+    tot += xor32(tot);
+    if (hl == 0) row_tot[r] = tot;
+  }
+  __syncthreads();
+  const int nrows = min(128, a.Nq - qb * 128);
+  float* out = reinterpret_cast<float*>(a.out) + ((int64_t)bh * a.nqb + qb) * nkb;
+  for (int kb = tid; kb < nkb; kb += 256) {
+    float acc = 0.f;
+    for (int rr = 0; rr < nrows; ++rr) acc += sums[rr * NKBMAX + kb] / fmaxf(row_tot[rr], 1e-6f);
+    out[kb] = acc / (float)nrows;
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Exact block mass, f32 inputs: fp32 matrix cores (v_mfma_f32_32x32x2_f32).
+// Work-group = 4 waves = 128 rows.  Each 128-key block is staged as four 32-key fp32
+// sub-tiles (rows padded to 132 floats).  The contraction index of MFMA step s is
+// d = s for lanes 0-31 and d = s + 64 for lanes 32-63, so four consecutive steps read
+// one 16-byte LDS vector.
+// ------------------------------------------------------------------------------------
+template <int NKBMAX>
+__global__ __launch_bounds__(256) void block_mass_f32_kernel(PoolArgs a) {
+  constexpr int KP = 132;  // padded row length (floats)
+  __shared__ float lds_k[32 * KP];
+  __shared__ float sums[128 * NKBMAX];
+  __shared__ float row_tot[128];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int qb = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int nkb = a.nkb;
+
+  const float* qbase = (const float*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]);
+  const float* kbase = (const float*)a.k + ((int64_t)b * a.ks[0] + (int64_t)h * a.ks[1]);
+
+  const int r = wave * 32 + l32;
+  const int qrow = qb * 128 + r;
+  float qf[64];
+#pragma unroll
+  for (int s4 = 0; s4 < 16; ++s4) {
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (qrow < a.Nq)
+      v = *reinterpret_cast<const f32x4*>(qbase + (int64_t)qrow * a.qs[2] + hl * 64 + s4 * 4);
+    qf[4 * s4] = v[0]; qf[4 * s4 + 1] = v[1]; qf[4 * s4 + 2] = v[2]; qf[4 * s4 + 3] = v[3];
+  }
+
+  const float c = a.scale * kLog2e;
+  float m_ref = neg_inf();
+  float* my = sums + r * NKBMAX;
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    float ps = 0.f;
+    for (int t = 0; t < 4; ++t) {
+      const int key0 = kb * 128 + t * 32;
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 32 * 32 / 256; ++i) {
+        const int id = i * 256 + tid;
+        const int row = id >> 5, c4 = id & 31;
+        const int key = key0 + row;
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (key < a.Nk) v = *reinterpret_cast<const f32x4*>(kbase + (int64_t)key * a.ks[2] + c4 * 4);
+        *reinterpret_cast<f32x4*>(lds_k + row * KP + c4 * 4) = v;
+      }
+      __syncthreads();
+      f32x16 s = f32x16{};
+#pragma unroll
+      for (int s4 = 0; s4 < 16; ++s4) {
+        const f32x4 av = *reinterpret_cast<const f32x4*>(lds_k + l32 * KP + hl * 64 + s4 * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          s = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], qf[4 * s4 + e], s, 0, 0, 0);
+      }
+      if (key0 + 32 > a.Nk) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (key0 + 8 * (j >> 2) + 4 * hl + (j & 3) >= a.Nk) s[j] = neg_inf();
+      }
+      float mx = neg_inf();
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[j]);
+      mx = fmaxf(mx, xor32(mx)) * c;
+      if (mx > m_ref + kRescaleMargin) {
+        const float f = fast_exp2(m_ref - mx);
+        for (int j = hl; j < kb; j += 2) my[j] *= f;
+        ps *= f;
+        m_ref = mx;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) ps += fast_exp2(__builtin_fmaf(s[j], c, -m_ref));
+    }
+    ps += xor32(ps);
+    if (hl == 0) my[kb] = ps;
+  }
+  __syncthreads();
+  {
+    float tot = 0.f;
+    for (int j = hl; j < nkb; j += 2) tot += my[j];
+    tot += xor32(tot);
+    if (hl == 0) row_tot[r] = tot;
+  }
+  __syncthreads();
+  const int nrows = min(128, a.Nq - qb * 128);
+  float* out = reinterpret_cast<float*>(a.out) + ((int64_t)bh * a.nqb + qb) * nkb;
+  for (int kb = tid; kb < nkb; kb += 256) {
+    float acc = 0.f;
+    for (int rr = 0; rr < nrows; ++rr) acc += sums[rr * NKBMAX + kb] / fmaxf(row_tot[rr], 1e-6f);
+    out[kb] = acc / (float)nrows;
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Max-pool map (16-bit inputs).
+// ------------------------------------------------------------------------------------
+template <int CT>
+__device__ __forceinline__ float round_to(float x);
+template <>
+__device__ __forceinline__ float round_to<kBF16>(float x) {
+  return (float)(__bf16)x;
+}
+template <>
+__device__ __forceinline__ float round_to<kF16>(float x) {
+  return (float)(_Float16)x;
+}
+
+template <int IT, int NKBMAX>
+__global__ __launch_bounds__(256) void max_pool_kernel(PoolArgs a) {
+  constexpr int CT = IT;
+  constexpr int D = 128;
+  constexpr int ES = ElemSize<IT>::value;
+  constexpr int KC = D / 8;
+  __shared__ u32x4 lds_k[128 * KC];
+  __shared__ float rmax[128 * NKBMAX];  // q.dtype-rounded block maxima, log2 domain
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int qb = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int hk = h / (a.H / a.Hk);
+  const int nkb = a.nkb;
+  const int kb_end = a.causal ? min(nkb, qb + 1) : nkb;
+
+  const char* qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * ES;
+  const char* kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)hk * a.ks[1]) * ES;
+
+  const int r = wave * 32 + l32;
+  const int qrow = qb * 128 + r;
+  u32x4 qf[D / 16];
+  load_q_operand<IT, CT, D>(qf, qbase, a.qs[2], qrow, a.Nq, hl);
+  const int prow = k_row_perm(l32);
+  const int fk = k_swz(prow);
+  // The reference forms qk_scale = fp32(sm_scale) * fp32(1.44269504).
+  const float qk_scale = a.scale * 1.44269504f;
+  float m = neg_inf();
+  float* my = rmax + r * NKBMAX;
+
+  for (int kb = 0; kb < kb_end; ++kb) {
+    const int key0 = kb * 128;
+    __syncthreads();
+    stage_k_tile<IT, CT, D, 256>(lds_k, kbase, a.ks[2], key0, a.Nk, tid);
+    __syncthreads();
+    f32x16 s[4];
+    qk_tile<CT, D>(lds_k, qf, prow, fk, hl, s);
+    const bool ragged = key0 + 128 > a.Nk;
+    const bool diag = a.causal && kb == qb;
+    if (ragged || diag) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key = key0 + t * 32 + tile_key(hl, j);
+          if (diag && qrow < key) s[t][j] += -1.0e6f;
+          if (key >= a.Nk) s[t][j] = neg_inf();
+        }
+    }
+    float mx = neg_inf();
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
+    mx = fmaxf(mx, xor32(mx)) * qk_scale;
+    m = fmaxf(m, mx);
+    if (hl == 0) my[kb] = round_to<CT>(mx);
+  }
+  __syncthreads();
+  // m_r of every row, in the K-tile storage.
+  float* mrow = reinterpret_cast<float*>(lds_k);
+  if (hl == 0) mrow[r] = m;
+  __syncthreads();
+  const int nrows = min(128, a.Nq - qb * 128);
+  float* colmax = reinterpret_cast<float*>(lds_k) + 128;  // nkb values
+  for (int kb = tid; kb < kb_end; kb += 256) {
+    float best = 0.f;
+    for (int rr = 0; rr < nrows; ++rr) best = fmaxf(best, fast_exp2(rmax[rr * NKBMAX + kb] - mrow[rr]));
+    colmax[kb] = round_to<CT>(best);
+  }
+  __syncthreads();
+  // Row normalisation in q.dtype: sum (fp32 accumulate, rounded), then divide.
+  float* total_sh = colmax + 256;
+  if (wave == 0) {
+    float part = 0.f;
+    for (int kb = lane; kb < kb_end; kb += 64) part += colmax[kb];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+    if (lane == 0) *total_sh = round_to<CT>(part);
+  }
+  __syncthreads();
+  const float total = *total_sh;
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * a.nqb + qb) * nkb;
+  for (int kb = tid; kb < nkb; kb += 256) {
+    const float v = kb < kb_end ? colmax[kb] / total : 0.f;
+    uint32_t bits = pack2<CT>(v, 0.f) & 0xffffu;
+    out[kb] = (uint16_t)bits;
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Mean-pooled scores.  Pass 1: per-block means of Q and K (replicate-padded tail).
+// ------------------------------------------------------------------------------------
+template <int IT>
+__global__ __launch_bounds__(128) void mean_pool_rows_kernel(PoolArgs a, int which) {
+  // blockIdx.x = block index, blockIdx.y = bh; thread = d.
+  const int blk = blockIdx.x, bh = blockIdx.y, d = threadIdx.x;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int N = which == 0 ? a.Nq : a.Nk;
+  const int nb = which == 0 ? a.nqb : a.nkb;
+  const int64_t* st = which == 0 ? a.qs : a.ks;
+  const void* base = which == 0 ? a.q : a.k;
+  const int D = blockDim.x;
+  const int bs = 128;
+  float acc = 0.f;
+  for (int i = 0; i < bs; ++i) {
+    const int n = min(blk * bs + i, N - 1);
+    const int64_t off = (int64_t)b * st[0] + (int64_t)h * st[1] + (int64_t)n * st[2] + d;
+    float x;
+    if (IT == kF32) x = reinterpret_cast<const float*>(base)[off];
+    else if (IT == kBF16) x = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(base)[off]);
+    else x = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(base)[off]);
+    acc += x;
+  }
+  float* dst = a.ws + (which == 0 ? 0 : (int64_t)a.B * a.H * a.nqb * D);
+  dst[((int64_t)bh * nb + blk) * D + d] = acc / (float)bs;
+}
+
+// Pass 2: one wave per (bh, qb) row: dot products against every pooled key, softmax.
+__global__ __launch_bounds__(64) void mean_pool_scores_kernel(PoolArgs a, int D) {
+  const int qb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
+  const float* qp = a.ws + ((int64_t)bh * a.nqb + qb) * D;
+  const float* kp = a.ws + (int64_t)a.B * a.H * a.nqb * D + (int64_t)bh * a.nkb * D;
+  float* out = reinterpret_cast<float*>(a.out) + ((int64_t)bh * a.nqb + qb) * a.nkb;
+  float mx = neg_inf();
+  for (int kb = lane; kb < a.nkb; kb += 64) {
+    float acc = 0.f;
+    for (int d = 0; d < D; ++d) acc = __builtin_fmaf(qp[d], kp[(int64_t)kb * D + d], acc);
+    const float sc = acc * a.scale;
+    out[kb] = sc;
+    mx = fmaxf(mx, sc);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  float sum = 0.f;
+  for (int kb = lane; kb < a.nkb; kb += 64) {
+    const float e = expf(out[kb] - mx);
+    out[kb] = e;
+    sum += e;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  for (int kb = lane; kb < a.nkb; kb += 64) out[kb] = out[kb] / sum;
+}
+
+// ------------------------------------------------------------------------------------
+hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream) {
+  (void)D;
+  if (a.B * a.H * a.nqb == 0) return hipSuccess;
+  const dim3 grid(a.nqb, a.B * a.H);
+  if (dtype == kF32) {
+    if (a.nkb <= 64) block_mass_f32_kernel<64><<<grid, 256, 0, stream>>>(a);
+    else block_mass_f32_kernel<256><<<grid, 256, 0, stream>>>(a);
+    return hipGetLastError();
+  }
+  if (dtype == kBF16) {
+    if (a.nkb <= 64) block_mass_kernel<kBF16, kBF16, 64><<<grid, 256, 0, stream>>>(a);
+    else block_mass_kernel<kBF16, kBF16, 256><<<grid, 256, 0, stream>>>(a);
+  } else {
+    if (a.nkb <= 64) block_mass_kernel<kF16, kF16, 64><<<grid, 256, 0, stream>>>(a);
+    else block_mass_kernel<kF16, kF16, 256><<<grid, 256, 0, stream>>>(a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_max_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream) {
+  (void)D;
+  if (a.B * a.H * a.nqb == 0) return hipSuccess;
+  const dim3 grid(a.nqb, a.B * a.H);
+  if (dtype == kBF16) {
+    if (a.nkb <= 64) max_pool_kernel<kBF16, 64><<<grid, 256, 0, stream>>>(a);
+    else max_pool_kernel<kBF16, 256><<<grid, 256, 0, stream>>>(a);
+  } else {
+    if (a.nkb <= 64) max_pool_kernel<kF16, 64><<<grid, 256, 0, stream>>>(a);
+    else max_pool_kernel<kF16, 256><<<grid, 256, 0, stream>>>(a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_mean_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream) {
+  if (a.B * a.H == 0) return hipSuccess;
+  for (int which = 0; which < 2; ++which) {
+    const dim3 grid(which == 0 ? a.nqb : a.nkb, a.B * a.H);
+    if (dtype == kF32) mean_pool_rows_kernel<kF32><<<grid, D, 0, stream>>>(a, which);
+    else if (dtype == kBF16) mean_pool_rows_kernel<kBF16><<<grid, D, 0, stream>>>(a, which);
+    else mean_pool_rows_kernel<kF16><<<grid, D, 0, stream>>>(a, which);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  mean_pool_scores_kernel<<<dim3(a.nqb, a.B * a.H), 64, 0, stream>>>(a, D);
+  return hipGetLastError();
+}
+
+}  // namespace sa

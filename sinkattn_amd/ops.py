@@ -1,0 +1,282 @@
+"""Torch-facing wrappers of the libsinkattn kernels.
+
+Each wrapper checks device/dtype/shape, allocates outputs with torch on the inputs'
+device, and launches on torch's current stream.  Inputs on the CPU, or any other
+condition the kernels cannot handle, raise: there is no CPU or eager fallback.
+"""
+from __future__ import annotations
+
+import math
+import weakref
+from dataclasses import dataclass
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from sinkattn_amd import _lib
+
+KERNEL_BLOCK = 128
+
+
+def _cdiv(a: int, b: int) -> int:
+    return (a + b - 1) // b
+
+
+def _require_cuda(name: str, *tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(f"{name}: tensors must be on a ROCm GPU (got {t.device})")
+
+
+def _kernel_operand(t: torch.Tensor) -> torch.Tensor:
+    """Return t if the kernels can address it in place, else a contiguous copy."""
+    s = t.stride()
+    ok = (
+        t.dim() == 4
+        and s[3] == 1
+        and all(x % 8 == 0 and x >= 0 for x in s[:3])
+        and t.data_ptr() % 16 == 0
+    )
+    return t if ok else t.contiguous()
+
+
+@dataclass
+class BlockSparsePlan:
+    """Per-(b, h, q-block) ascending key-block lists built from a bool block mask."""
+
+    counts: torch.Tensor  # int32 [B*H*nqb]
+    idx: torch.Tensor  # int32 [B*H*nqb*nkb]
+    order: torch.Tensor  # int32 [B*H*nqb], rows by descending count
+    shape: Tuple[int, int, int, int]  # B, H, nqb, nkb
+
+    @property
+    def listed_tiles(self) -> torch.Tensor:
+        return self.counts.sum()
+
+
+def block_sparse_plan(block_mask: torch.Tensor) -> BlockSparsePlan:
+    """Turn a bool [B, H, nqb, nkb] mask into the kernel's lists (one small launch)."""
+    _require_cuda("block_sparse_plan", block_mask)
+    if block_mask.dim() != 4:
+        raise ValueError(f"block mask must be [B, H, nqb, nkb], got {tuple(block_mask.shape)}")
+    m = block_mask
+    if m.dtype != torch.bool and m.dtype != torch.uint8:
+        m = m != 0
+    B, H, nqb, nkb = (int(x) for x in m.shape)
+    dev = m.device
+    rows = B * H * nqb
+    counts = torch.empty(rows, dtype=torch.int32, device=dev)
+    idx = torch.empty(rows * nkb, dtype=torch.int32, device=dev)
+    order = torch.empty(rows, dtype=torch.int32, device=dev)
+    L = _lib.lib()
+    with torch.cuda.device(dev):
+        st = _lib.strides4(m)
+        _lib.check(
+            L.sinkattn_block_sparse_plan(
+                m.data_ptr(), st, B, H, nqb, nkb, counts.data_ptr(), idx.data_ptr(),
+                order.data_ptr(), _lib.stream_ptr(dev),
+            ),
+            "block_sparse_plan",
+        )
+    return BlockSparsePlan(counts, idx, order, (B, H, nqb, nkb))
+
+
+class _PlanCache:
+    """Plans keyed by mask tensor identity and version (runtime masks are cached objects)."""
+
+    def __init__(self) -> None:
+        self._entries: Dict[int, tuple] = {}
+
+    def get(self, mask: torch.Tensor) -> BlockSparsePlan:
+        key = id(mask)
+        ent = self._entries.get(key)
+        sig = (mask._version, mask.data_ptr(), tuple(mask.shape), tuple(mask.stride()), mask.device)
+        if ent is not None:
+            ref, esig, plan = ent
+            if ref() is mask and esig == sig:
+                return plan
+        plan = block_sparse_plan(mask)
+        entries = self._entries
+        ref = weakref.ref(mask, lambda _r, k=key: entries.pop(k, None))
+        entries[key] = (ref, sig, plan)
+        return plan
+
+    def clear(self) -> None:
+        self._entries.clear()
+
+
+PLAN_CACHE = _PlanCache()
+
+
+def block_sparse_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    plan: BlockSparsePlan,
+    softmax_scale: Optional[float] = None,
+    return_lse: bool = True,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Block-sparse attention forward on [B, H, N, D] views.
+
+    Returns out as a [B, H, Nq, D] view of [B, Nq, H, D] memory (the layout the
+    reference's varlen call returns) and lse as fp32 [B, H, Nq] (or None).
+    """
+    _require_cuda("block_sparse_attention", q, k, v)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be [B, H, N, D]")
+    B, H, Nq, D = (int(x) for x in q.shape)
+    Nk = int(k.shape[2])
+    if tuple(k.shape) != (B, H, Nk, D) or tuple(v.shape) != (B, H, Nk, D):
+        raise ValueError(f"k/v shapes {tuple(k.shape)}/{tuple(v.shape)} do not match q {tuple(q.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q, k, v must share a dtype")
+    dt = _lib.dtype_code(q.dtype)
+    nqb, nkb = _cdiv(Nq, KERNEL_BLOCK), _cdiv(Nk, KERNEL_BLOCK)
+    if plan.shape != (B, H, nqb, nkb):
+        raise ValueError(f"block mask shape {plan.shape} does not match [{B}, {H}, {nqb}, {nkb}]")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    qk, kk, vk = _kernel_operand(q), _kernel_operand(k), _kernel_operand(v)
+    out = torch.empty((B, Nq, H, D), dtype=q.dtype, device=q.device).permute(0, 2, 1, 3)
+    lse = torch.empty((B, H, Nq), dtype=torch.float32, device=q.device) if return_lse else None
+    L = _lib.lib()
+    with torch.cuda.device(q.device):
+        _lib.check(
+            L.sinkattn_block_sparse_fwd(
+                qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), dt, B, H, Nq, Nk, D,
+                _lib.strides4(qk), _lib.strides4(kk), _lib.strides4(vk),
+                out.data_ptr(), _lib.strides4(out), _lib.ptr(lse),
+                plan.counts.data_ptr(), plan.idx.data_ptr(), plan.order.data_ptr(),
+                nqb, nkb, float(softmax_scale), _lib.stream_ptr(q.device),
+            ),
+            "block_sparse_fwd",
+        )
+    return out, lse
+
+
+def block_mass_scores(q: torch.Tensor, k: torch.Tensor, block_size: int = 128,
+                      scale: Optional[float] = None) -> torch.Tensor:
+    """Exact per-(q-block, k-block) mean softmax mass, fp32 [B, H, nqb, nkb]."""
+    _require_cuda("block_mass_scores", q, k)
+    B, H, Nq, D = (int(x) for x in q.shape)
+    Nk = int(k.shape[2])
+    if tuple(k.shape) != (B, H, Nk, D):
+        raise ValueError(f"k shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    if q.dtype != k.dtype:
+        raise TypeError("q and k must share a dtype")
+    dt = _lib.dtype_code(q.dtype)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    qk, kk = _kernel_operand(q), _kernel_operand(k)
+    out = torch.empty((B, H, _cdiv(Nq, block_size), _cdiv(Nk, block_size)), dtype=torch.float32,
+                      device=q.device)
+    L = _lib.lib()
+    with torch.cuda.device(q.device):
+        _lib.check(
+            L.sinkattn_block_mass_pool(
+                qk.data_ptr(), kk.data_ptr(), dt, B, H, Nq, Nk, D, _lib.strides4(qk),
+                _lib.strides4(kk), int(block_size), float(scale), out.data_ptr(),
+                _lib.stream_ptr(q.device),
+            ),
+            "block_mass_pool",
+        )
+    return out
+
+
+def max_pool_scores(q: torch.Tensor, k: torch.Tensor, sm_scale: float, block_size: int = 128,
+                    causal: bool = False) -> torch.Tensor:
+    """Row-normalised max-pool map in q.dtype, [B, H, nd, nd]."""
+    _require_cuda("max_pool_scores", q, k)
+    B, H, N, D = (int(x) for x in q.shape)
+    Hk = int(k.shape[1])
+    if int(k.shape[0]) != B or int(k.shape[2]) != N or int(k.shape[3]) != D:
+        raise ValueError(f"k shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    if q.dtype != k.dtype:
+        raise TypeError("q and k must share a dtype")
+    dt = _lib.dtype_code(q.dtype)
+    qk, kk = _kernel_operand(q), _kernel_operand(k)
+    nd = _cdiv(N, block_size)
+    po = torch.empty((B, H, nd, nd), dtype=q.dtype, device=q.device)
+    L = _lib.lib()
+    with torch.cuda.device(q.device):
+        _lib.check(
+            L.sinkattn_max_pool(
+                qk.data_ptr(), kk.data_ptr(), dt, B, H, Hk, N, D, _lib.strides4(qk),
+                _lib.strides4(kk), int(block_size), float(sm_scale), int(bool(causal)),
+                po.data_ptr(), _lib.stream_ptr(q.device),
+            ),
+            "max_pool",
+        )
+    return po
+
+
+def mean_pool_scores(q: torch.Tensor, k: torch.Tensor, block_size: int = 128,
+                     scale: Optional[float] = None) -> torch.Tensor:
+    """softmax(mean-pooled Q . mean-pooled K^T * scale), fp32 [B, H, nqb, nkb]."""
+    _require_cuda("mean_pool_scores", q, k)
+    B, H, Nq, D = (int(x) for x in q.shape)
+    Nk = int(k.shape[2])
+    if tuple(k.shape) != (B, H, Nk, D):
+        raise ValueError(f"k shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    if q.dtype != k.dtype:
+        raise TypeError("q and k must share a dtype")
+    dt = _lib.dtype_code(q.dtype)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    qk, kk = _kernel_operand(q), _kernel_operand(k)
+    L = _lib.lib()
+    ws_bytes = int(L.sinkattn_mean_pool_workspace_bytes(B, H, Nq, Nk, D, int(block_size)))
+    ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=q.device)
+    out = torch.empty((B, H, _cdiv(Nq, block_size), _cdiv(Nk, block_size)), dtype=torch.float32,
+                      device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(
+            L.sinkattn_mean_pool_scores(
+                qk.data_ptr(), kk.data_ptr(), dt, B, H, Nq, Nk, D, _lib.strides4(qk),
+                _lib.strides4(kk), int(block_size), float(scale), ws.data_ptr(), out.data_ptr(),
+                _lib.stream_ptr(q.device),
+            ),
+            "mean_pool_scores",
+        )
+    return out
+
+
+def coverage_mask(
+    scores: torch.Tensor,
+    coverage: float,
+    keep_diagonal: bool,
+    req_q: int = 0,
+    req_k: int = 0,
+    video_residual_text_blocks: Optional[int] = None,
+    want_lists: bool = False,
+):
+    """Coverage mask of fp32 [H, nq, nk] scores (on the GPU).
+
+    Returns the bool mask, or (mask, counts int32 [H, nq], idx int32 [H, nq, nk]) when
+    want_lists is set.
+    """
+    _require_cuda("coverage_mask", scores)
+    if scores.dim() != 3:
+        raise ValueError(f"Expected [heads, blocks_q, blocks_k] scores, got {tuple(scores.shape)}")
+    s = scores.float().contiguous()
+    H, nq, nk = (int(x) for x in s.shape)
+    mask = torch.empty((H, nq, nk), dtype=torch.bool, device=s.device)
+    counts = torch.empty((H, nq), dtype=torch.int32, device=s.device) if want_lists else None
+    idx = torch.empty((H, nq, nk), dtype=torch.int32, device=s.device) if want_lists else None
+    mode = 0 if video_residual_text_blocks is None else 1
+    tb = 0 if video_residual_text_blocks is None else int(video_residual_text_blocks)
+    L = _lib.lib()
+    ws = torch.empty(max(int(L.sinkattn_coverage_mask_workspace_bytes(H, nq)), 1), dtype=torch.uint8,
+                     device=s.device)
+    with torch.cuda.device(s.device):
+        _lib.check(
+            L.sinkattn_coverage_mask(
+                s.data_ptr(), H, nq, nk, float(coverage), int(bool(keep_diagonal)), int(req_q),
+                int(req_k), mode, tb, mask.data_ptr(), _lib.ptr(counts), _lib.ptr(idx),
+                ws.data_ptr(), _lib.stream_ptr(s.device),
+            ),
+            "coverage_mask",
+        )
+    if want_lists:
+        return mask, counts, idx
+    return mask

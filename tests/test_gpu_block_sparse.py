@@ -1,0 +1,161 @@
+"""GPU parity of the block-sparse attention forward (sinkattn_block_sparse_fwd) against
+the fp32 dense masked-softmax oracle (oracle/torch_ref.dense_masked_attention).
+
+Tolerance (north star): max |out - ref| <= 2e-2 and mean |out - ref| <= 1e-3; lse is
+compared in fp32 to 2e-2 absolute.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import torch_ref
+from sinkattn_amd import ops
+from sinkattn_amd import sparse_attention as sa
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 1e-3
+
+
+def _inputs(B, H, Nq, Nk, D, dtype, seed, sink_keys=0, sink_scale=8.0, layout="bhsd"):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, Nq, D, generator=g)
+    k = torch.randn(B, H, Nk, D, generator=g)
+    v = torch.randn(B, H, Nk, D, generator=g)
+    if sink_keys:
+        k[:, :, :sink_keys] *= sink_scale
+    dev = "cuda"
+    if layout == "bshd":  # [B, N, H, D] memory viewed as [B, H, N, D]
+        q = q.transpose(1, 2).contiguous().transpose(1, 2)
+        k = k.transpose(1, 2).contiguous().transpose(1, 2)
+        v = v.transpose(1, 2).contiguous().transpose(1, 2)
+    return q.to(dev, dtype), k.to(dev, dtype), v.to(dev, dtype)
+
+
+def _random_mask(B, H, nqb, nkb, density, seed, diag=True, col0=True, empty_rows=0):
+    g = torch.Generator().manual_seed(seed)
+    m = torch.rand(B, H, nqb, nkb, generator=g) < density
+    if diag:
+        d = torch.arange(min(nqb, nkb))
+        m[:, :, d, d] = True
+    if col0:
+        m[..., 0] = True
+    for i in range(empty_rows):
+        m[0, 0, (7 * i) % nqb, :] = False
+    return m.cuda()
+
+
+def _check(out, lse, q, k, v, mask, rows=None, scale=None):
+    ref_o, ref_l = torch_ref.dense_masked_attention(q, k, v, mask, scale=scale, rows=rows)
+    o = out.float().cpu()
+    l = lse.float().cpu()
+    if rows is not None:
+        o = o[:, :, rows.cpu()]
+        l = l[:, :, rows.cpu()]
+    err = (o - ref_o).abs()
+    assert err.max().item() <= MAX_ABS, err.max().item()
+    assert err.mean().item() <= MEAN_ABS, err.mean().item()
+    fin = torch.isfinite(ref_l)
+    assert torch.equal(fin, torch.isfinite(l))
+    assert (l[fin] - ref_l[fin]).abs().max().item() <= 2e-2
+    assert torch.equal(o[~fin.unsqueeze(-1).expand_as(o)], torch.zeros_like(o[~fin.unsqueeze(-1).expand_as(o)]))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("N", [256, 1000])
+def test_small_random_masks(dtype, N):
+    q, k, v = _inputs(1, 3, N, N, 128, dtype, seed=N)
+    nb = math.ceil(N / 128)
+    mask = _random_mask(1, 3, nb, nb, 0.4, seed=1)
+    plan = ops.block_sparse_plan(mask)
+    out, lse = ops.block_sparse_attention(q, k, v, plan)
+    torch.cuda.synchronize()
+    _check(out, lse, q, k, v, mask)
+
+
+def test_config1_shape_fp32_with_sinks():
+    # B=1, H=12, N=4096, d=128, fp32, 4 sink keys scaled 8x.
+    q, k, v = _inputs(1, 12, 4096, 4096, 128, torch.float32, seed=0, sink_keys=4)
+    mask = _random_mask(1, 12, 32, 32, 0.25, seed=3)
+    out, lse = sa._block_sparse_attn(q, k, v, mask, return_lse=True)
+    torch.cuda.synchronize()
+    assert lse.shape == (1, 12, 4096, 1) and lse.dtype == torch.float32
+    rows = torch.randperm(4096, generator=torch.Generator().manual_seed(0))[:512].sort().values
+    _check(out, lse[..., 0], q, k, v, mask, rows=rows)
+
+
+def test_full_mask_equals_dense_sdpa():
+    q, k, v = _inputs(2, 4, 640, 640, 128, torch.bfloat16, seed=5)
+    mask = torch.ones(2, 4, 5, 5, dtype=torch.bool, device="cuda")
+    out, _ = sa._block_sparse_attn(q, k, v, mask, return_lse=False)
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float().cpu(), k.float().cpu(), v.float().cpu())
+    err = (out.float().cpu() - ref).abs()
+    assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
+
+
+def test_diagonal_mask_is_block_local_attention():
+    q, k, v = _inputs(1, 2, 512, 512, 128, torch.bfloat16, seed=6)
+    mask = torch.eye(4, dtype=torch.bool, device="cuda").expand(1, 2, 4, 4).contiguous()
+    out, lse = sa._block_sparse_attn(q, k, v, mask)
+    qs, ks, vs = (t.float().cpu().view(1, 2, 4, 128, 128) for t in (q, k, v))
+    ref = torch.nn.functional.scaled_dot_product_attention(qs, ks, vs).view(1, 2, 512, 128)
+    err = (out.float().cpu() - ref).abs()
+    assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
+
+
+def test_empty_rows_ragged_and_strided_bshd():
+    # ragged N (last block 50 keys), rows with no listed block, [B,N,H,D] memory views
+    q, k, v = _inputs(2, 3, 690, 690, 128, torch.bfloat16, seed=7, layout="bshd")
+    mask = _random_mask(2, 3, 6, 6, 0.3, seed=8, diag=False, col0=False, empty_rows=2)
+    out, lse = sa._block_sparse_attn(q, k, v, mask)
+    torch.cuda.synchronize()
+    _check(out, lse[..., 0], q, k, v, mask)
+    assert out.stride() == (690 * 3 * 128, 128, 3 * 128, 1)
+
+
+def test_head_dim_64_and_cross_lengths():
+    q, _, _ = _inputs(1, 2, 300, 300, 64, torch.bfloat16, seed=9)
+    _, k, v = _inputs(1, 2, 1092, 1092, 64, torch.bfloat16, seed=10)
+    mask = _random_mask(1, 2, 3, 9, 0.5, seed=11)
+    out, lse = sa._block_sparse_attn(q, k, v, mask)
+    torch.cuda.synchronize()
+    _check(out, lse[..., 0], q, k, v, mask)
+
+
+def test_plan_lists_and_order():
+    mask = _random_mask(2, 3, 7, 9, 0.35, seed=12, diag=False, col0=False, empty_rows=1)
+    plan = ops.block_sparse_plan(mask)
+    counts = plan.counts.cpu()
+    idx = plan.idx.cpu().view(-1, 9)
+    flat = mask.cpu().view(-1, 9)
+    for r in range(flat.shape[0]):
+        want = torch.nonzero(flat[r]).flatten().to(torch.int32)
+        assert counts[r].item() == want.numel()
+        assert torch.equal(idx[r, : want.numel()], want)
+    order = plan.order.cpu()
+    assert torch.equal(order.sort().values, torch.arange(flat.shape[0], dtype=torch.int32))
+    assert (counts[order][:-1] >= counts[order][1:]).all()
+
+
+def test_bad_mask_shape_raises():
+    q, k, v = _inputs(1, 2, 256, 256, 128, torch.bfloat16, seed=1)
+    with pytest.raises(ValueError):
+        sa._block_sparse_attn(q, k, v, torch.ones(1, 2, 3, 2, dtype=torch.bool, device="cuda"))
+
+
+@pytest.mark.slow
+def test_wan_config2_full_size_rows_subsampled():
+    # BASELINE config 2 at full size: B=2, H=12, N=32760 (last block 120), bf16, sinks at
+    # frame-0 positions, 20% seeded mask + diagonal + column 0.  The oracle evaluates 48
+    # rows per (b, h) spread over the sequence, including the ragged last block.
+    B, H, N = 2, 12, 32760
+    q, k, v = _inputs(B, H, N, N, 128, torch.bfloat16, seed=20)
+    g = torch.Generator().manual_seed(21)
+    sinks = torch.randint(0, 1560, (8,), generator=g)
+    k[:, :, sinks.cuda()] *= 6.0
+    mask = _random_mask(B, H, 256, 256, 0.2, seed=22)
+    out, lse = sa._block_sparse_attn(q, k, v, mask)
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.randperm(N - 120, generator=g)[:40], torch.arange(N - 8, N)]).sort().values
+    _check(out, lse[..., 0], q, k, v, mask, rows=rows)

@@ -1,0 +1,127 @@
+"""GPU coverage-mask kernel: bit-exact against the reference semantics on CPU torch
+(oracle/torch_ref.coverage_mask, the same torch calls as sparse_attention.py:268-376,
+run on this machine's CPU) and against the C restatement (oracle/coverage_ref.c).
+The per-row index lists and counts must describe the same mask.
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import torch_ref
+from sinkattn_amd import ops
+from sinkattn_amd import sparse_attention as sa
+
+pytestmark = pytest.mark.gpu
+
+
+def _scores(H, nq, nk, kind, seed):
+    rng = np.random.default_rng(seed)
+    if kind == "dirichlet":
+        x = rng.gamma(0.3, size=(H * nq, nk))
+    elif kind == "ties":
+        x = rng.integers(0, 5, size=(H * nq, nk)) / 7.0
+    elif kind == "sinky":  # exact-mass-like rows: a few large blocks, long small tail
+        x = rng.gamma(0.05, size=(H * nq, nk)) + 1e-4 * rng.random((H * nq, nk))
+        x[:, 0] += 2.0
+    elif kind == "uniform":
+        x = np.ones((H * nq, nk))
+    else:
+        raise ValueError(kind)
+    s = torch.from_numpy(x.astype(np.float32)).view(H, nq, nk)
+    return s / s.sum(-1, keepdim=True).clamp_min(1e-30)
+
+
+def _check_lists(mask, counts, idx):
+    m = mask.cpu()
+    c = counts.cpu()
+    i = idx.cpu()
+    assert torch.equal(c, m.sum(-1).to(torch.int32))
+    H, nq, nk = m.shape
+    for h in range(H):
+        for q in range(0, nq, max(1, nq // 16)):
+            want = torch.nonzero(m[h, q]).flatten().to(torch.int32)
+            assert torch.equal(i[h, q, : want.numel()], want)
+
+
+CONFIGS = [
+    ("c1", (12, 32, 32), {}),
+    ("c2", (12, 256, 256), {}),
+    ("c4", (30, 132, 132), dict(text_length=512, force_text=True)),
+    ("c4_video", (30, 132, 132), dict(text_length=512, force_text=True, mode="video_residual")),
+    ("nodiag", (4, 40, 17), dict(keep_diagonal=False)),
+    ("wide_rows", (2, 8, 600), {}),
+    ("short_rows", (3, 9, 5), dict(coverage=0.5)),
+]
+
+
+@pytest.mark.parametrize("name,shape,kw", CONFIGS, ids=[c[0] for c in CONFIGS])
+@pytest.mark.parametrize("kind", ["dirichlet", "ties", "sinky", "uniform"])
+def test_mask_bit_exact(oracle_lib, name, shape, kw, kind):
+    s = _scores(*shape, kind, seed=zlib.crc32(f"{name}/{kind}".encode()) % 1000)
+    ref = torch_ref.coverage_mask(s, **kw)
+    cfg = sa.SinkSparseConfig(
+        offline_direct_coverage=kw.get("coverage", 0.85),
+        keep_diagonal=kw.get("keep_diagonal", True),
+        text_length=kw.get("text_length", 0),
+        force_text_global_attention=kw.get("force_text", False),
+        offline_text_video_coverage_mode=kw.get("mode", "joint"),
+    )
+    ours_cpu_in = sa._build_direct_mean_coverage_mask(s, cfg)  # CPU tensor in, like the reference
+    assert ours_cpu_in.device.type == "cpu" and ours_cpu_in.dtype == torch.bool
+    assert torch.equal(ours_cpu_in, ref)
+    # direct kernel call with lists
+    rq = rk = 0
+    if kw.get("force_text"):
+        tb = -(-kw["text_length"] // 128)
+        rq, rk = min(tb, shape[1]), min(tb, shape[2])
+    vt = min(-(-kw["text_length"] // 128), shape[1], shape[2]) if kw.get("mode") == "video_residual" else None
+    mask, counts, idx = ops.coverage_mask(s.cuda(), kw.get("coverage", 0.85), kw.get("keep_diagonal", True),
+                                          rq, rk, vt, want_lists=True)
+    assert torch.equal(mask.cpu(), ref)
+    _check_lists(mask, counts, idx)
+
+
+def test_empty_row_fallback_quirk_on_gpu(oracle_lib):
+    # an all-zero row without diagonal empties -> every row's top-1 bit is overwritten
+    nk = 16
+    rows = np.zeros((3, nk), np.float32)
+    rows[0, 5] = 0.9
+    rows[0, :5] = 0.02
+    rows[1, :] = 1.0 / nk  # tie at the top: top-1 comes from the exact std::sort order
+    s = torch.from_numpy(rows).view(1, 3, nk)
+    ref = torch_ref.coverage_mask(s, keep_diagonal=False)
+    cfg = sa.SinkSparseConfig(keep_diagonal=False)
+    assert torch.equal(sa._build_direct_mean_coverage_mask(s.cuda(), cfg).cpu(), ref)
+    assert torch.equal(torch.from_numpy(oracle_lib.coverage_mask(s.numpy(), 0.85, False)), ref)
+
+
+def test_many_tie_rows_exact_permutation(oracle_lib):
+    # small-integer scores: ties straddle the cut in most rows
+    rng = np.random.default_rng(0)
+    for nk in (32, 132, 256):
+        x = rng.integers(1, 4, size=(8 * 64, nk)).astype(np.float32)
+        s = torch.from_numpy(x).view(8, 64, nk)
+        ref = torch_ref.coverage_mask(s)
+        got = ops.coverage_mask(s.cuda(), 0.85, True).cpu()
+        assert torch.equal(got, ref), nk
+        assert np.array_equal(oracle_lib.coverage_mask(s.numpy()), ref.numpy())
+
+
+def test_calibrator_end_to_end_matches_reference_math():
+    # record() twice on small Wan-like layers, then build the package
+    torch.manual_seed(0)
+    cfg = sa.SinkSparseConfig(pooling_mode="exact")
+    cal = sa.SinkMaskCalibrator(cfg)
+    for step in range(2):
+        for layer in range(2):
+            q = torch.randn(2, 3, 640, 128, device="cuda", dtype=torch.bfloat16)
+            k = torch.randn(2, 3, 640, 128, device="cuda", dtype=torch.bfloat16)
+            cal.record(layer, q, k, k)
+    pkg = cal.build_package()
+    assert pkg["version"] == 3 and set(pkg["sink_masks"]) == {"0", "1"}
+    for key, mean in pkg["mean_scores"].items():
+        assert mean.device.type == "cpu"
+        assert torch.equal(pkg["sink_masks"][key], torch_ref.coverage_mask(mean))
+        assert pkg["counts"][key] == 2

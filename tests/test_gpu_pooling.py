@@ -1,0 +1,153 @@
+"""GPU parity of the block-score kernels.
+
+exact mode  vs oracle/torch_ref.exact_block_mass (fp32 restatement of
+            sparse_attention.py:145-227): elementwise rtol 1e-5 (atol 1e-8); rows of the
+            map sum to 1.
+max mode    vs oracle/torch_ref.max_pool_map (closed form with the reference's bf16
+            rounding points): equal, or within one bf16 ulp where a rounding boundary
+            is crossed (bit-level Triton behaviour is not pinned).
+mean mode   vs oracle/torch_ref.mean_pool_scores: rtol 1e-5.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import torch_ref
+from sinkattn_amd import ops
+from sinkattn_amd import sparse_attention as sa
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-8
+
+
+def _qk(B, H, Nq, Nk, dtype, seed, sinks=0, sink_scale=8.0, sink_at_end=False):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, Nq, 128, generator=g)
+    k = torch.randn(B, H, Nk, 128, generator=g)
+    if sinks:
+        if sink_at_end:
+            k[:, :, -sinks:] *= sink_scale
+        else:
+            k[:, :, :sinks] *= sink_scale
+    return q.to(dtype), k.to(dtype)
+
+
+def _close(ours, ref):
+    ours = ours.cpu().double()
+    ref = ref.cpu().double()
+    bad = (ours - ref).abs() > ATOL + RTOL * ref.abs()
+    assert not bad.any(), f"{bad.sum().item()} elements, max rel {((ours - ref).abs() / ref.abs().clamp_min(1e-30)).max().item():.3g}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("N", [384, 1000])
+def test_exact_mass_small(dtype, N):
+    q, k = _qk(1, 2, N, N, dtype, seed=N, sinks=4)
+    ours = ops.block_mass_scores(q.cuda(), k.cuda())
+    ref = torch_ref.exact_block_mass(q, k)
+    _close(ours, ref)
+    assert torch.allclose(ours.sum(-1).cpu(), torch.ones(1, 2, ours.shape[2]), atol=1e-5)
+
+
+def test_exact_mass_config1_fp32():
+    # [1,12,4096,128] fp32 with 4 sink keys scaled 8x -> [1,12,32,32]
+    q, k = _qk(1, 12, 4096, 4096, torch.float32, seed=0, sinks=4)
+    cfg = sa.SinkSparseConfig(pooling_mode="exact")
+    ours = sa._compute_block_scores(q.cuda(), k.cuda(), k.cuda(), cfg)
+    assert ours.shape == (1, 12, 32, 32) and ours.dtype == torch.float32
+    ref = torch_ref.exact_block_mass(q, k)
+    _close(ours, ref)
+
+
+def test_exact_mass_rescale_path_sinks_last():
+    # the running maximum keeps rising (sinks at the end, growing key norms): exercises
+    # the per-row rescaling of earlier key-block sums
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, 2, 512, 128, generator=g)
+    k = torch.randn(1, 2, 1500, 128, generator=g) * torch.linspace(0.2, 3.0, 1500).view(1, 1, -1, 1)
+    for dt in (torch.bfloat16, torch.float32):
+        qq, kk = q.to(dt), k.to(dt)
+        _close(ops.block_mass_scores(qq.cuda(), kk.cuda()), torch_ref.exact_block_mass(qq, kk))
+
+
+def test_exact_mass_closed_forms():
+    # Q = 0: uniform softmax -> mass = |kb| / N (last block 120 of 32760 -> 120/N)
+    N = 1016  # 7 full blocks + 120
+    q = torch.zeros(1, 1, 256, 128, dtype=torch.bfloat16)
+    k = torch.randn(1, 1, N, 128).to(torch.bfloat16)
+    m = ops.block_mass_scores(q.cuda(), k.cuda()).cpu()
+    want = torch.tensor([128.0] * 7 + [120.0]) / N
+    assert torch.allclose(m[0, 0], want.expand(2, -1), rtol=1e-5, atol=0)
+    # one dominant key: all the mass in its block
+    k2 = torch.zeros(1, 1, N, 128)
+    k2[0, 0, 300] = 50.0
+    q2 = torch.ones(1, 1, 256, 128)
+    m2 = ops.block_mass_scores(q2.cuda().bfloat16(), k2.cuda().bfloat16()).cpu()
+    assert torch.allclose(m2[0, 0, :, 2], torch.ones(2), atol=1e-6)
+
+
+def test_exact_mass_vs_fp64():
+    q, k = _qk(2, 2, 700, 900, torch.bfloat16, seed=4, sinks=3)
+    ours = ops.block_mass_scores(q.cuda(), k.cuda()).cpu().double()
+    ref = torch_ref.exact_block_mass_fp64(q, k)
+    assert ((ours - ref).abs() <= 2e-5 * ref.abs() + 1e-9).all()
+
+
+@pytest.mark.slow
+def test_exact_mass_wan_shape_one_head():
+    # Wan config 2/3 shape per (b, h): N = 32760 (ragged 120), bf16 -> [256, 256]
+    q, k = _qk(1, 1, 32760, 32760, torch.bfloat16, seed=5, sinks=16)
+    ours = ops.block_mass_scores(q.cuda(), k.cuda()).cpu()
+    assert ours.shape == (1, 1, 256, 256)
+    assert torch.allclose(ours.sum(-1), torch.ones(1, 1, 256), atol=2e-5)
+    rows = [0, 1, 97, 255]
+    ref = torch_ref.exact_block_mass(q[:, :, [r * 128 + i for r in rows for i in range(128 if r < 255 else 120)]], k)
+    # ref rows are the selected q-blocks in order
+    _close(ours[:, :, rows], ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_max_pool_vs_closed_form(dtype, causal):
+    q, k = _qk(1, 4, 1024, 1024, dtype, seed=7, sinks=2)
+    sm = 1.0 / math.sqrt(128)
+    ours = ops.max_pool_scores(q.cuda(), k.cuda(), sm, causal=causal).cpu()
+    ref = torch_ref.max_pool_map(q, k, sm, causal=causal)
+    assert ours.dtype == dtype
+    diff = (ours.float() - ref.float()).abs()
+    ulp = ref.float().abs() * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10) + 1e-30
+    assert (diff <= ulp).all(), diff.max().item()
+    assert (diff == 0).float().mean().item() > 0.9
+    # exact (unrounded) formula agrees to q.dtype precision
+    ex = torch_ref.max_pool_map(q, k, sm, causal=causal, exact=True)
+    assert torch.allclose(ours.double(), ex, rtol=3e-2, atol=1e-3)
+
+
+def test_attn_with_pooling_api_and_gqa():
+    from sinkattention.pooling_kernel import attn_with_pooling
+    q, _ = _qk(1, 4, 512, 512, torch.bfloat16, seed=8)
+    _, k = _qk(1, 2, 512, 512, torch.bfloat16, seed=9)
+    o, po = attn_with_pooling(q.cuda(), k.cuda(), k.cuda(), False, 0.088, 128)
+    assert o.shape == q.shape and not o.any()
+    ref = torch_ref.max_pool_map(q, k, 0.088)
+    assert ((po.cpu().float() - ref.float()).abs() <= ref.float().abs() * 2 ** -7 + 1e-30).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_mean_mode(dtype):
+    q, k = _qk(2, 3, 1000, 700, dtype, seed=10)
+    cfg = sa.SinkSparseConfig(pooling_mode="mean")
+    ours = sa._compute_block_scores(q.cuda(), k.cuda(), k.cuda(), cfg).cpu()
+    ref = torch_ref.mean_pool_scores(q, k)
+    assert torch.allclose(ours, ref, rtol=1e-5, atol=1e-7)
+
+
+def test_pooling_mode_dispatch():
+    q, k = _qk(1, 2, 256, 256, torch.bfloat16, seed=11)
+    qc, kc = q.cuda(), k.cuda()
+    with pytest.raises(ValueError):
+        sa._compute_block_scores(qc, kc, kc, sa.SinkSparseConfig(pooling_mode="bogus"))
+    t = sa._compute_block_scores(qc, kc, kc, sa.SinkSparseConfig(pooling_mode="triton"))
+    assert t.dtype == torch.float32 and t.shape == (1, 2, 2, 2)
