@@ -158,6 +158,374 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_kernel(FwdArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------------
+// D = 128, bf16/f16: K and V tiles go global -> LDS by buffer DMA (no staging
+// registers; rows >= Nk read as zero through the buffer bounds), and V^T is read from
+// the row-major V tile with the gfx950 transpose read ds_read_b64_tr_b16.  K and V are
+// double-staged against each other: K(i+1) streams in while softmax(i) and PV(i) run,
+// V(i+1) while S(i+1) runs.  LDS layout: 128 rows x 16 chunks of 16 bytes per tile,
+// physical chunk = logical ^ (row & 15) for K and logical ^ (4 * (row & 3)) for V, which
+// keeps the 16-lane K reads and the 32-lane transpose reads on distinct banks.
+// ------------------------------------------------------------------------------------
+template <int CT>
+__global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a) {
+  constexpr int DS = 8, DT = 4;
+  __shared__ u32x4 lds_k[2048];
+  __shared__ u32x4 lds_v[2048];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  // Work-item values are uniform: keep them in scalar registers so the list walk uses
+  // scalar loads and never enters the vector-memory counter the DMA waits rely on.
+  const int item = __builtin_amdgcn_readfirstlane(a.order ? a.order[blockIdx.x] : (int)blockIdx.x);
+  const int bh = item / a.nqb;
+  const int qb = item - bh * a.nqb;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int cnt = __builtin_amdgcn_readfirstlane(a.counts[item]);
+  // The plan is read-only for the kernel's lifetime: read it through the constant
+  // address space so the list walk compiles to scalar loads.
+  const SA_CONST int32_t* list = (const SA_CONST int32_t*)(a.idx + (int64_t)item * a.nkb);
+
+  const char* qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * 2;
+  const char* kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)h * a.ks[1]) * 2;
+  const char* vbase = (const char*)a.v + ((int64_t)b * a.vs[0] + (int64_t)h * a.vs[1]) * 2;
+  const uint32_t kstride = (uint32_t)a.ks[2] * 2, vstride = (uint32_t)a.vs[2] * 2;
+
+  const int qrow = qb * 128 + wave * 32 + l32;
+  u32x4 qf[DS];
+  load_q_operand<CT, CT, 128>(qf, qbase, a.qs[2], qrow, a.Nq, hl);
+
+  // DMA: instruction j of wave w fills tile rows 16j + 4w + lane/16 (LDS bytes
+  // [(256j + 64w) * 16, +1024)); the swizzle of those rows does not depend on j.
+  const int drow = 4 * wave + (lane >> 4);
+  const uint32_t k_off = (uint32_t)drow * kstride + (uint32_t)(((lane & 15) ^ (drow & 15)) * 16);
+  const uint32_t v_off = (uint32_t)drow * vstride + (uint32_t)(((lane & 15) ^ (4 * (drow & 3))) * 16);
+  // LDS read addresses (bytes).  K: MFMA row t*32 + k_row_perm(l32), chunk 2ds + hl.
+  const int prow = k_row_perm(l32);
+  uint32_t ka[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) ka[ds] = (uint32_t)(prow * 256 + (((2 * ds + hl) ^ (prow & 15)) * 16));
+  // V^T via transpose reads: 16-lane group g, lane s in group -> source row
+  // 8*(g/2) + 4r + s/4 (+16u + 32t), columns dt*32 + 16*(g%2) + 4*(s%4) .. +3.
+  uint32_t va[DT][2];
+  {
+    const int g = lane >> 4, sl = lane & 15;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int row = 8 * (g >> 1) + 4 * r + (sl >> 2);
+        const int chunk = dt * 4 + 2 * (g & 1) + ((sl & 3) >> 1);
+        const int phys = chunk ^ (4 * (row & 3));
+        va[dt][r] = (uint32_t)(row * 256 + phys * 16 + (sl & 1) * 8);
+      }
+  }
+  SA_LDS char* lk = (SA_LDS char*)lds_k;
+  SA_LDS char* lv = (SA_LDS char*)lds_v;
+
+  auto issue_k = [&](int kb) {
+    const int key0 = kb * 128;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(kbase + (int64_t)key0 * kstride, (uint32_t)(a.Nk - key0) * kstride);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      dma16(rs, (SA_LDS void*)(lk + (256 * j + 64 * wave) * 16), k_off + (uint32_t)j * 16u * kstride);
+  };
+  auto issue_v = [&](int kb) {
+    const int key0 = kb * 128;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(vbase + (int64_t)key0 * vstride, (uint32_t)(a.Nk - key0) * vstride);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      dma16(rs, (SA_LDS void*)(lv + (256 * j + 64 * wave) * 16), v_off + (uint32_t)j * 16u * vstride);
+  };
+
+  f32x16 o[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) o[i] = f32x16{};
+  float m_run = neg_inf();
+  float l_run = 0.f;
+  const float c = a.scale * kLog2e;
+
+  if (cnt > 0) {
+    const int kb0 = list[0];
+    issue_k(kb0);
+    issue_v(kb0);
+  }
+  for (int it = 0; it < cnt; ++it) {
+    const int key0 = list[it] * 128;
+    const bool next = it + 1 < cnt;
+    wait_vmcnt<8>();  // this wave's K(it) has landed (V(it) may still be in flight)
+    __builtin_amdgcn_s_barrier();
+    f32x16 s[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s[t] = f32x16{};
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const u32x4 av = *(SA_LDS const u32x4*)(lk + ka[ds] + t * 8192);
+        s[t] = mfma32x32x16<CT>(av, qf[ds], s[t]);
+      }
+    __builtin_amdgcn_s_barrier();  // every wave is done reading K(it)
+    const int kb_next = next ? list[it + 1] : 0;
+    if (next) issue_k(kb_next);
+
+    if (key0 + 128 > a.Nk) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (key0 + t * 32 + tile_key(hl, j) >= a.Nk) s[t][j] = neg_inf();
+    }
+    float mx = neg_inf();
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
+    mx = fmaxf(mx, xor32(mx));
+    const float m_new = fmaxf(m_run, mx * c);
+    if (m_new != m_run) {
+      const float alpha = fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < DT; ++i) o[i] *= alpha;
+      m_run = m_new;
+    }
+    u32x4 p[4][2];
+    float lsum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v0 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e], c, -m_run));
+          const float v1 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e + 1], c, -m_run));
+          lsum += v0 + v1;
+          p[t][u][e] = pack2<CT>(v0, v1);
+        }
+    l_run += lsum;
+
+    if (next)
+      wait_vmcnt<8>();  // V(it) landed; K(it+1) may be in flight
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const uint32_t off = t * 8192 + u * 4096;
+          const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][0] + off));
+          const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][1] + off));
+          const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
+          const u32x4 av = u32x4{y0[0], y0[1], y1[0], y1[1]};
+          o[dt] = mfma32x32x16<CT>(av, p[t][u], o[dt]);
+        }
+    __builtin_amdgcn_s_barrier();  // every wave is done reading V(it)
+    if (next) issue_v(kb_next);
+  }
+
+  const float l = l_run + xor32(l_run);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (qrow < a.Nq) {
+    char* obase = (char*)a.out + ((int64_t)b * a.os[0] + (int64_t)h * a.os[1] + (int64_t)qrow * a.os[2]) * 2;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = dt * 32 + 8 * g + 4 * hl;
+        store4<CT>(obase + d * 2, o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                   o[dt][4 * g + 3] * inv);
+      }
+    if (a.lse != nullptr && hl == 0)
+      a.lse[((int64_t)b * a.H + h) * a.Nq + qrow] = cnt > 0 ? (m_run + __log2f(l)) * kLn2 : pos_inf();
+  }
+}
+
+// fp32 operands: every value is split as x = hi + lo with hi = bf16(x) and
+// lo = bf16(x - hi); each product is formed as hi*hi + hi*lo + lo*hi on the bf16 matrix
+// cores (about 16 mantissa bits), for QK^T and for PV (P split the same way).  Same
+// tiling as block_sparse_fwd_kernel; the hi and lo tiles of K and V^T double the LDS.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  const float h0 = (float)(__bf16)x0, h1 = (float)(__bf16)x1;
+  hi = pack2<kBF16>(h0, h1);
+  lo = pack2<kBF16>(x0 - h0, x1 - h1);
+}
+
+__device__ __forceinline__ void split8(const float* p, u32x4& hi, u32x4& lo) {
+  const f32x4 a = reinterpret_cast<const f32x4*>(p)[0];
+  const f32x4 b = reinterpret_cast<const f32x4*>(p)[1];
+  uint32_t h[4], l[4];
+  split_pair(a[0], a[1], h[0], l[0]);
+  split_pair(a[2], a[3], h[1], l[1]);
+  split_pair(b[0], b[1], h[2], l[2]);
+  split_pair(b[2], b[3], h[3], l[3]);
+  hi = u32x4{h[0], h[1], h[2], h[3]};
+  lo = u32x4{l[0], l[1], l[2], l[3]};
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void block_sparse_fwd_f32_kernel(FwdArgs a) {
+  constexpr int KC = D / 8, DS = D / 16, DT = D / 32;
+  __shared__ u32x4 kh[128 * KC], kl[128 * KC];
+  __shared__ u32x4 vh[D * 16], vl[D * 16];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int item = a.order ? a.order[blockIdx.x] : (int)blockIdx.x;
+  const int bh = item / a.nqb;
+  const int qb = item - bh * a.nqb;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int cnt = a.counts[item];
+  const int32_t* list = a.idx + (int64_t)item * a.nkb;
+  const float* qbase = (const float*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]);
+  const float* kbase = (const float*)a.k + ((int64_t)b * a.ks[0] + (int64_t)h * a.ks[1]);
+  const float* vbase = (const float*)a.v + ((int64_t)b * a.vs[0] + (int64_t)h * a.vs[1]);
+
+  const int qrow = qb * 128 + wave * 32 + l32;
+  u32x4 qh[DS], ql[DS];
+#pragma unroll
+  for (int s = 0; s < DS; ++s) {
+    qh[s] = u32x4{0, 0, 0, 0};
+    ql[s] = u32x4{0, 0, 0, 0};
+    if (qrow < a.Nq) split8(qbase + (int64_t)qrow * a.qs[2] + s * 16 + hl * 8, qh[s], ql[s]);
+  }
+  f32x16 o[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) o[i] = f32x16{};
+  float m_run = neg_inf(), l_run = 0.f;
+  const float c = a.scale * kLog2e;
+  const int prow = k_row_perm(l32);
+  const int fk = k_swz(prow);
+
+  for (int it = 0; it < cnt; ++it) {
+    const int key0 = list[it] * 128;
+    __syncthreads();
+#pragma unroll
+    for (int c8 = 0; c8 < D / 16; ++c8) {
+      const int id = c8 * 256 + tid;
+      const int row = id / KC, ch = id % KC;
+      const int key = key0 + row;
+      u32x4 hi = u32x4{0, 0, 0, 0}, lo = u32x4{0, 0, 0, 0};
+      if (key < a.Nk) split8(kbase + (int64_t)key * a.ks[2] + ch * 8, hi, lo);
+      kh[row * KC + (ch ^ k_swz(row))] = hi;
+      kl[row * KC + (ch ^ k_swz(row))] = lo;
+    }
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      const int id = i * 256 + tid;
+      const int dp = id % (D / 2), kg = id / (D / 2);
+      uint32_t wh[8], wl[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int key = key0 + kg * 8 + e;
+        f32x2 x = f32x2{0.f, 0.f};
+        if (key < a.Nk) x = *reinterpret_cast<const f32x2*>(vbase + (int64_t)key * a.vs[2] + 2 * dp);
+        split_pair(x[0], x[1], wh[e], wl[e]);
+      }
+      u32x4 eh, oh, el, ol;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        eh[j] = (wh[2 * j] & 0xffffu) | (wh[2 * j + 1] << 16);
+        oh[j] = (wh[2 * j] >> 16) | (wh[2 * j + 1] & 0xffff0000u);
+        el[j] = (wl[2 * j] & 0xffffu) | (wl[2 * j + 1] << 16);
+        ol[j] = (wl[2 * j] >> 16) | (wl[2 * j + 1] & 0xffff0000u);
+      }
+      const int d0 = 2 * dp;
+      vh[d0 * 16 + (kg ^ v_swz(d0))] = eh;
+      vh[(d0 + 1) * 16 + (kg ^ v_swz(d0 + 1))] = oh;
+      vl[d0 * 16 + (kg ^ v_swz(d0))] = el;
+      vl[(d0 + 1) * 16 + (kg ^ v_swz(d0 + 1))] = ol;
+    }
+    __syncthreads();
+
+    f32x16 s[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s[t] = f32x16{};
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int idx = (t * 32 + prow) * KC + ((2 * ds + hl) ^ fk);
+        const u32x4 ah = kh[idx], al = kl[idx];
+        s[t] = mfma32x32x16<kBF16>(ah, qh[ds], s[t]);
+        s[t] = mfma32x32x16<kBF16>(ah, ql[ds], s[t]);
+        s[t] = mfma32x32x16<kBF16>(al, qh[ds], s[t]);
+      }
+    if (key0 + 128 > a.Nk) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (key0 + t * 32 + tile_key(hl, j) >= a.Nk) s[t][j] = neg_inf();
+    }
+    float mx = neg_inf();
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
+    mx = fmaxf(mx, xor32(mx));
+    const float m_new = fmaxf(m_run, mx * c);
+    const float alpha = fast_exp2(m_run - m_new);
+    l_run *= alpha;
+#pragma unroll
+    for (int i = 0; i < DT; ++i) o[i] *= alpha;
+    u32x4 ph[4][2], pl[4][2];
+    float lsum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v0 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e], c, -m_new));
+          const float v1 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e + 1], c, -m_new));
+          lsum += v0 + v1;
+          uint32_t hv, lv;
+          split_pair(v0, v1, hv, lv);
+          ph[t][u][e] = hv;
+          pl[t][u][e] = lv;
+        }
+    l_run += lsum;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int R = dt * 32 + l32;
+      const int fv = v_swz(R);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int idx = R * 16 + ((4 * t + 2 * u + hl) ^ fv);
+          const u32x4 ah = vh[idx], al = vl[idx];
+          o[dt] = mfma32x32x16<kBF16>(ah, ph[t][u], o[dt]);
+          o[dt] = mfma32x32x16<kBF16>(ah, pl[t][u], o[dt]);
+          o[dt] = mfma32x32x16<kBF16>(al, ph[t][u], o[dt]);
+        }
+    }
+  }
+
+  const float l = l_run + xor32(l_run);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (qrow < a.Nq) {
+    float* obase = (float*)a.out + ((int64_t)b * a.os[0] + (int64_t)h * a.os[1] + (int64_t)qrow * a.os[2]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = dt * 32 + 8 * g + 4 * hl;
+        store4<kF32>(obase + d, o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                     o[dt][4 * g + 3] * inv);
+      }
+    if (a.lse != nullptr && hl == 0)
+      a.lse[((int64_t)b * a.H + h) * a.Nq + qrow] = cnt > 0 ? (m_run + __log2f(l)) * kLn2 : pos_inf();
+  }
+}
+
 // One wave per (b, h, q-block) row: ballot-compact the mask row into an ascending list.
 __global__ __launch_bounds__(256) void plan_rows_kernel(PlanArgs a) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -215,7 +583,7 @@ template <int IT, int CT>
 static hipError_t launch_fwd_dt(const FwdArgs& a, int D, hipStream_t stream) {
   const int grid = (int)(a.B * a.H * a.nqb);
   if (D == 128)
-    block_sparse_fwd_kernel<IT, CT, 128><<<grid, 256, 0, stream>>>(a);
+    block_sparse_fwd_d128_kernel<CT><<<grid, 256, 0, stream>>>(a);
   else
     block_sparse_fwd_kernel<IT, CT, 64><<<grid, 256, 0, stream>>>(a);
   return hipGetLastError();
@@ -226,7 +594,14 @@ hipError_t launch_block_sparse_fwd(const FwdArgs& a, int dtype, int D, hipStream
   switch (dtype) {
     case kBF16: return launch_fwd_dt<kBF16, kBF16>(a, D, stream);
     case kF16: return launch_fwd_dt<kF16, kF16>(a, D, stream);
-    default: return launch_fwd_dt<kF32, kBF16>(a, D, stream);
+    default: {
+      const int grid = (int)(a.B * a.H * a.nqb);
+      if (D == 128)
+        block_sparse_fwd_f32_kernel<128><<<grid, 256, 0, stream>>>(a);
+      else
+        block_sparse_fwd_f32_kernel<64><<<grid, 256, 0, stream>>>(a);
+      return hipGetLastError();
+    }
   }
 }
 

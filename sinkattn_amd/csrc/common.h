@@ -13,6 +13,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 enum DType { kBF16 = 0, kF16 = 1, kF32 = 2 };
 
@@ -136,6 +137,28 @@ __device__ __forceinline__ void store4<kF32>(void* p, float a, float b, float c,
   f32x4 v;
   v[0] = a; v[1] = b; v[2] = c; v[3] = d;
   *reinterpret_cast<f32x4*>(p) = v;
+}
+
+// s_waitcnt with only a vector-memory count (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
+// lgkmcnt[11:8], vmcnt[15:14]); expcnt/lgkmcnt left at "no wait".
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+#define SA_LDS __attribute__((address_space(3)))
+#define SA_CONST __attribute__((address_space(4)))
+
+// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes per lane from rsrc+voffset into LDS at lds_wave_base + lane*16.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, SA_LDS void* lds_wave_base,
+                                      uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds_wave_base, 16, voffset, 0, 0, 0);
 }
 
 }  // namespace sa

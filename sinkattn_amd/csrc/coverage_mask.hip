@@ -23,6 +23,10 @@
 #include "common.h"
 #include "kernels.h"
 
+// Every product and sum here must round exactly like the reference's CPU arithmetic:
+// no fused multiply-adds (e.g. coverage * total - selected must round the product).
+#pragma clang fp contract(off)
+
 namespace sa {
 
 constexpr int kMaskMaxN = 1024;

@@ -58,7 +58,9 @@ def _check(out, lse, q, k, v, mask, rows=None, scale=None):
     assert err.mean().item() <= MEAN_ABS, err.mean().item()
     fin = torch.isfinite(ref_l)
     assert torch.equal(fin, torch.isfinite(l))
-    assert (l[fin] - ref_l[fin]).abs().max().item() <= 2e-2
+    # lse from the drop-in API is cast to q.dtype like the reference's; allow that rounding
+    rnd = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}.get(lse.dtype, 0.0)
+    assert ((l[fin] - ref_l[fin]).abs() <= 2e-2 + rnd * ref_l[fin].abs()).all()
     assert torch.equal(o[~fin.unsqueeze(-1).expand_as(o)], torch.zeros_like(o[~fin.unsqueeze(-1).expand_as(o)]))
 
 

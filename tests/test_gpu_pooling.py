@@ -120,9 +120,10 @@ def test_max_pool_vs_closed_form(dtype, causal):
     ulp = ref.float().abs() * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10) + 1e-30
     assert (diff <= ulp).all(), diff.max().item()
     assert (diff == 0).float().mean().item() > 0.9
-    # exact (unrounded) formula agrees to q.dtype precision
+    # the unrounded formula agrees up to the reference's own rounding of the log2-domain
+    # block maxima to q.dtype (|R| ~ 40 -> bf16 ulp 0.25 -> up to 2^0.125 in the ratio)
     ex = torch_ref.max_pool_map(q, k, sm, causal=causal, exact=True)
-    assert torch.allclose(ours.double(), ex, rtol=3e-2, atol=1e-3)
+    assert torch.allclose(ours.double(), ex, rtol=0.2, atol=1e-3)
 
 
 def test_attn_with_pooling_api_and_gqa():
