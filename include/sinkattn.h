@@ -84,14 +84,18 @@ int sinkattn_block_sparse_fwd(const void* q, const void* k, const void* v, int d
  *     P = softmax_rows(scale * Q K^T)                  (fp32, over all Nk keys)
  *     out[b,h,qb,kb] = mean over the rows r of q-block qb of  sum_{j in kb} P[r,j]
  * out is fp32 [B,H,nqb,nkb] contiguous, nqb = ceil(Nq/block), nkb = ceil(Nk/block).
- * bf16/f16 inputs use the matrix cores (exact products, fp32 sums); f32 inputs use the
- * fp32 matrix path.  block_size must be 128.  Requires nkb <= 256 for bf16/f16
- * (128-row work-groups) and nkb <= 256 for f32 (64-row work-groups).
+ * bf16/f16 inputs use the bf16/f16 matrix cores (products are exact, sums fp32) and a
+ * device workspace of sinkattn_block_mass_pool_workspace_bytes() bytes (per-row block
+ * sums of the resident work-groups, queried for the current device); f32 inputs use the
+ * fp32 matrix cores and need no workspace (pass NULL).  block_size must be 128 and
+ * nkb <= 256 for f32.
  * ---------------------------------------------------------------------------------- */
+size_t sinkattn_block_mass_pool_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nk,
+                                                int64_t block_size, int dtype);
 int sinkattn_block_mass_pool(const void* q, const void* k, int dtype,
                              int64_t B, int64_t H, int64_t Nq, int64_t Nk, int64_t D,
                              const int64_t q_strides[4], const int64_t k_strides[4],
-                             int64_t block_size, float scale, float* out,
+                             int64_t block_size, float scale, float* out, void* workspace,
                              void* stream);
 
 /* ------------------------------------------------------------------------------------

@@ -36,10 +36,13 @@ SIGNATURES = {
          _c_i64_4, _c_i64_4, _c_i64_4, _c_p, _c_i64_4, _c_p, _c_p, _c_p, _c_p,
          _c_i64, _c_i64, ctypes.c_float, _c_p],
     ),
+    "sinkattn_block_mass_pool_workspace_bytes": (
+        ctypes.c_size_t, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int],
+    ),
     "sinkattn_block_mass_pool": (
         ctypes.c_int,
         [_c_p, _c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64_4, _c_i64_4,
-         _c_i64, ctypes.c_float, _c_p, _c_p],
+         _c_i64, ctypes.c_float, _c_p, _c_p, _c_p],
     ),
     "sinkattn_max_pool": (
         ctypes.c_int,

@@ -100,6 +100,11 @@ int sinkattn_block_sparse_fwd(const void* q, const void* k, const void* v, int d
   if ((rc = check_operand("v", v, v_strides)) != 0) return rc;
   if ((rc = check_operand("out", out, out_strides)) != 0) return rc;
   if (counts == nullptr || idx == nullptr) return fail("fwd: null plan");
+  if (dtype != SINKATTN_F32 && D == 128) {
+    if (k_strides[2] < D || v_strides[2] < D) return fail("fwd: k/v row stride below the head dim");
+    if (Nk * k_strides[2] * 2 >= (int64_t)1 << 31 || Nk * v_strides[2] * 2 >= (int64_t)1 << 31)
+      return fail("fwd: one head of k or v spans more than 2 GiB");
+  }
   sa::FwdArgs a{};
   a.q = q;
   a.k = k;
@@ -155,19 +160,35 @@ static int fill_pool_args(sa::PoolArgs& a, const char* who, const void* q, const
   return 0;
 }
 
+size_t sinkattn_block_mass_pool_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nk,
+                                                int64_t block_size, int dtype) {
+  if (dtype == SINKATTN_F32 || block_size <= 0) return 0;
+  const int64_t items = B * H * cdiv(Nq, block_size);
+  const int64_t groups = items < sa::block_mass_groups() ? items : sa::block_mass_groups();
+  return (size_t)(groups * cdiv(Nk, block_size) * 128 * (int64_t)sizeof(float));
+}
+
 int sinkattn_block_mass_pool(const void* q, const void* k, int dtype, int64_t B, int64_t H,
                              int64_t Nq, int64_t Nk, int64_t D, const int64_t q_strides[4],
                              const int64_t k_strides[4], int64_t block_size, float scale,
-                             float* out, void* stream) {
+                             float* out, void* workspace, void* stream) {
   sa::PoolArgs a{};
   int rc = fill_pool_args(a, "block_mass_pool", q, k, dtype, B, H, H, Nq, Nk, D, q_strides,
                           k_strides, block_size);
   if (rc != 0) return rc;
   if (Nk == 0) return fail("block_mass_pool: no keys");
-  if (a.nkb > 256) return fail("block_mass_pool: %d key blocks exceed the supported 256", a.nkb);
+  if (dtype == SINKATTN_F32 && a.nkb > 256)
+    return fail("block_mass_pool: %d key blocks exceed the supported 256 for f32", a.nkb);
   if (out == nullptr) return fail("block_mass_pool: null output");
+  if (dtype != SINKATTN_F32) {
+    if (workspace == nullptr) return fail("block_mass_pool: null workspace");
+    if (k_strides[2] < D) return fail("block_mass_pool: k row stride below the head dim");
+    if (Nk * k_strides[2] * 2 >= (int64_t)1 << 31)
+      return fail("block_mass_pool: one head of k spans more than 2 GiB");
+  }
   a.scale = scale;
   a.out = out;
+  a.ws = reinterpret_cast<float*>(workspace);
   return hip_status(sa::launch_block_mass_pool(a, dtype, (int)D, (hipStream_t)stream), "pool launch");
 }
 

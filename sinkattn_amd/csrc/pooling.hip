@@ -112,6 +112,138 @@ __global__ __launch_bounds__(256) void block_mass_kernel(PoolArgs a) {
 }
 
 // ------------------------------------------------------------------------------------
+// Exact block mass, 16-bit inputs, persistent work-groups (up to 3 per CU).
+// Each work-group walks (b, h, q-block) items; per item it streams every K tile into
+// LDS by buffer DMA (rows >= Nk read as zero and are masked), computes S^T for its 128
+// rows with the matrix cores and writes each row's per-key-block sum of
+// exp2(scale*log2e*s - m_ref) to its private workspace slot ws[kb][row].  m_ref is the
+// row maximum of the first tile; it only moves (and the row's earlier sums are
+// rescaled) if a tile's sum overflows 2^64, i.e. when scores rise more than ~64 log2
+// units above it.  The item's epilogue normalises every row by its total and averages
+// the rows of each key block.
+// ------------------------------------------------------------------------------------
+constexpr float kSumLimit = 1.8446744073709552e19f;  // 2^64
+
+template <int CT>
+__global__ __launch_bounds__(256, 3) void block_mass_persistent_kernel(PoolArgs a, int items) {
+  constexpr int DS = 8;
+  __shared__ u32x4 lds_k[2048];
+  __shared__ float row_inv[128];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int nkb = a.nkb;
+  float* ws = a.ws + (size_t)blockIdx.x * (size_t)nkb * 128;
+  const uint32_t kstride = (uint32_t)a.ks[2] * 2;
+  const int drow = 4 * wave + (lane >> 4);
+  const uint32_t k_off = (uint32_t)drow * kstride + (uint32_t)(((lane & 15) ^ (drow & 15)) * 16);
+  const int prow = k_row_perm(l32);
+  uint32_t ka[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) ka[ds] = (uint32_t)(prow * 256 + (((2 * ds + hl) ^ (prow & 15)) * 16));
+  SA_LDS char* lk = (SA_LDS char*)lds_k;
+  const float c = a.scale * kLog2e;
+  const int r = wave * 32 + l32;
+
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+    const int bh = item / a.nqb;
+    const int qb = item - bh * a.nqb;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const char* qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * 2;
+    const char* kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)h * a.ks[1]) * 2;
+    const int qrow = qb * 128 + r;
+    u32x4 qf[DS];
+    load_q_operand<CT, CT, 128>(qf, qbase, a.qs[2], qrow, a.Nq, hl);
+    float m_ref = neg_inf();
+    float l_tot = 0.f;
+
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int key0 = kb * 128;
+      __syncthreads();  // the previous tile (or item epilogue) is done with lds_k
+      {
+        const __amdgpu_buffer_rsrc_t rs =
+            make_rsrc(kbase + (int64_t)key0 * kstride, (uint32_t)(a.Nk - key0) * kstride);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          dma16(rs, (SA_LDS void*)(lk + (256 * j + 64 * wave) * 16), k_off + (uint32_t)j * 16u * kstride);
+      }
+      __syncthreads();  // waits for this group's DMA
+      f32x16 s[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) s[t] = f32x16{};
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const u32x4 av = *(SA_LDS const u32x4*)(lk + ka[ds] + t * 8192);
+          s[t] = mfma32x32x16<CT>(av, qf[ds], s[t]);
+        }
+      if (key0 + 128 > a.Nk) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            if (key0 + t * 32 + tile_key(hl, j) >= a.Nk) s[t][j] = neg_inf();
+      }
+      if (kb == 0) {  // reference maximum from the first tile (key 0 always exists)
+        float mx = neg_inf();
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
+        m_ref = fmaxf(mx, xor32(mx)) * c;
+      }
+      float ps = 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) ps += fast_exp2(__builtin_fmaf(s[t][j], c, -m_ref));
+      ps += xor32(ps);
+      if (!(ps <= kSumLimit)) {
+        // Rare: scores far above m_ref.  Move m_ref to this tile's maximum and rescale
+        // the row's earlier sums (the two lanes of the row split them by parity).
+        float mx = neg_inf();
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
+        mx = fmaxf(mx, xor32(mx)) * c;
+        const float f = fast_exp2(m_ref - mx);
+        for (int j = hl; j < kb; j += 2) ws[j * 128 + r] *= f;
+        l_tot *= f;
+        m_ref = mx;
+        ps = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) ps += fast_exp2(__builtin_fmaf(s[t][j], c, -m_ref));
+        ps += xor32(ps);
+      }
+      l_tot += ps;
+      if (hl == 0) ws[kb * 128 + r] = ps;
+    }
+
+    // Epilogue: out[kb] = mean over the block's rows of ws[kb][row] / total(row).
+    const int nrows = min(128, a.Nq - qb * 128);
+    if (hl == 0) row_inv[r] = (r < nrows) ? 1.f / fmaxf(l_tot, 1e-6f) : 0.f;
+    __syncthreads();
+    const float inv0 = row_inv[lane], inv1 = row_inv[lane + 64];
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(ws, (uint32_t)nkb * 512u);
+    float* out = reinterpret_cast<float*>(a.out) + ((int64_t)bh * a.nqb + qb) * nkb;
+    const float inv_n = 1.f / (float)nrows;
+    for (int kb = wave; kb < nkb; kb += 4) {
+      // coherent (L1-bypassing) loads of values other waves of the group wrote
+      const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4), 0, 1));
+      const float x1 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4 + 256), 0, 1));
+      float v = x0 * inv0 + x1 * inv1;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+      if (lane == 0) out[kb] = v * inv_n;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
 // Exact block mass, f32 inputs: fp32 matrix cores (v_mfma_f32_32x32x2_f32).
 // Work-group = 4 waves = 128 rows.  Each 128-key block is staged as four 32-key fp32
 // sub-tiles (rows padded to 132 floats).  The contraction index of MFMA step s is
@@ -375,6 +507,16 @@ __global__ __launch_bounds__(64) void mean_pool_scores_kernel(PoolArgs a, int D)
 }
 
 // ------------------------------------------------------------------------------------
+// Resident work-groups of the persistent block-mass kernel on the current device.
+int block_mass_groups() {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
+  }
+  return 3 * cus;
+}
+
 hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream) {
   (void)D;
   if (a.B * a.H * a.nqb == 0) return hipSuccess;
@@ -384,13 +526,12 @@ hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream
     else block_mass_f32_kernel<256><<<grid, 256, 0, stream>>>(a);
     return hipGetLastError();
   }
-  if (dtype == kBF16) {
-    if (a.nkb <= 64) block_mass_kernel<kBF16, kBF16, 64><<<grid, 256, 0, stream>>>(a);
-    else block_mass_kernel<kBF16, kBF16, 256><<<grid, 256, 0, stream>>>(a);
-  } else {
-    if (a.nkb <= 64) block_mass_kernel<kF16, kF16, 64><<<grid, 256, 0, stream>>>(a);
-    else block_mass_kernel<kF16, kF16, 256><<<grid, 256, 0, stream>>>(a);
-  }
+  const int items = a.B * a.H * a.nqb;
+  const int groups = min(items, block_mass_groups());
+  if (dtype == kBF16)
+    block_mass_persistent_kernel<kBF16><<<groups, 256, 0, stream>>>(a, items);
+  else
+    block_mass_persistent_kernel<kF16><<<groups, 256, 0, stream>>>(a, items);
   return hipGetLastError();
 }
 

@@ -172,10 +172,12 @@ def block_mass_scores(q: torch.Tensor, k: torch.Tensor, block_size: int = 128,
                       device=q.device)
     L = _lib.lib()
     with torch.cuda.device(q.device):
+        ws_bytes = int(L.sinkattn_block_mass_pool_workspace_bytes(B, H, Nq, Nk, int(block_size), dt))
+        ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=q.device) if ws_bytes else None
         _lib.check(
             L.sinkattn_block_mass_pool(
                 qk.data_ptr(), kk.data_ptr(), dt, B, H, Nq, Nk, D, _lib.strides4(qk),
-                _lib.strides4(kk), int(block_size), float(scale), out.data_ptr(),
+                _lib.strides4(kk), int(block_size), float(scale), out.data_ptr(), _lib.ptr(ws),
                 _lib.stream_ptr(q.device),
             ),
             "block_mass_pool",
