@@ -39,7 +39,12 @@ def _parse():
     p.add_argument("--density", type=float, default=0.20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true", help="skip dense/pooling/mask timings")
-    p.add_argument("--cpu-sample-qblocks", type=int, default=48)
+    p.add_argument("--cpu-sample-qblocks", type=int, default=1024,
+                   help="q-blocks of the layer the CPU baseline times (1024 = heads 0-3 of batch 0)")
+    p.add_argument("--only", choices=["all", "fa", "pool", "mask"], default="all",
+                   help="profiling aid: run just one kernel family (no JSON line unless 'all')")
+    p.add_argument("--copy-mb", type=int, default=0,
+                   help="profiling aid: first run a device copy of this many MiB (counter calibration)")
     return p.parse_args()
 
 
@@ -96,33 +101,37 @@ def cpu_baseline(torch, q, k, v, mask, n_qblocks, total_flops_layer):
     (b, h) = (0, 0); reported as the full-layer rate extrapolated from the sample."""
     from oracle import torch_ref  # noqa: F401  (the checker package; timed here as the CPU baseline)
 
-    qs = q[0, 0].float().cpu()
-    ks = k[0, 0].float().cpu()
-    vs = v[0, 0].float().cpu()
-    m = mask[0, 0].cpu()
-    N, D = qs.shape
+    N, D = int(q.shape[2]), int(q.shape[3])
+    nqb = int(mask.shape[2])
     scale = 1.0 / math.sqrt(D)
-    nqb = m.shape[0]
-    g = torch.Generator().manual_seed(0)
-    sample = torch.randperm(nqb, generator=g)[:n_qblocks].tolist()
+    heads = max(1, min(int(q.shape[1]), -(-n_qblocks // nqb)))
     flops = 0.0
-    t0 = time.perf_counter()
-    for qb in sample:
-        rows = slice(qb * 128, min((qb + 1) * 128, N))
-        kbs = torch.nonzero(m[qb]).flatten().tolist()
-        keys = torch.cat([torch.arange(kb * 128, min((kb + 1) * 128, N)) for kb in kbs])
-        s = (qs[rows] @ ks[keys].T) * scale
-        p = torch.softmax(s, dim=-1)
-        _ = p @ vs[keys]
-        flops += 4.0 * (rows.stop - rows.start) * keys.numel() * D
-    dt = time.perf_counter() - t0
+    done = 0
+    dt = 0.0
+    for h in range(heads):
+        qs, ks, vs = (t[0, h].float().cpu() for t in (q, k, v))
+        m = mask[0, h].cpu()
+        t0 = time.perf_counter()
+        for qb in range(nqb):
+            if done >= n_qblocks:
+                break
+            rows = slice(qb * 128, min((qb + 1) * 128, N))
+            kbs = torch.nonzero(m[qb]).flatten().tolist()
+            keys = torch.cat([torch.arange(kb * 128, min((kb + 1) * 128, N)) for kb in kbs])
+            s = (qs[rows] @ ks[keys].T) * scale
+            p = torch.softmax(s, dim=-1)
+            _ = p @ vs[keys]
+            flops += 4.0 * (rows.stop - rows.start) * keys.numel() * D
+            done += 1
+        dt += time.perf_counter() - t0
+    sample = range(done)
     rate = flops / dt
     return {
         "value": rate / 1e12,
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{len(sample)} q-blocks of (b,h)=(0,0) of the config-2 layer, fp32 torch on CPU "
+        "sample": f"{len(sample)} q-blocks (batch 0, heads 0-{heads - 1}) of the config-2 layer, fp32 torch on CPU "
                   f"({dt:.1f} s); full layer extrapolated: {total_flops_layer / rate * 1e3:.0f} ms",
         "ms_per_layer_extrapolated": total_flops_layer / rate * 1e3,
         "os_cpu_count": os.cpu_count(),
@@ -142,6 +151,12 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_mb:
+        src = torch.empty(args.copy_mb * (1 << 20) // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     q, k, v = wan_inputs(torch, dev)
     mask = wan_mask(torch, dev, args.density)
     B, H, N, D = q.shape
@@ -151,6 +166,15 @@ def main():
 
     def step():
         ops.block_sparse_attention(q, k, v, plan, return_lse=True)
+
+    if args.only != "all":
+        fn = {"fa": step, "pool": lambda: ops.block_mass_scores(q, k),
+              "mask": lambda: ops.coverage_mask(torch.rand(H, 256, 256, device=dev), 0.85, True)}[args.only]
+        for _ in range(args.warmup + args.steps):
+            fn()
+        torch.cuda.synchronize()
+        print(f"ran {args.only} x{args.warmup + args.steps}")
+        return
 
     ms = time_fn(torch, step, args.steps, args.warmup)
     tflops = flops / (ms * 1e-3) / 1e12

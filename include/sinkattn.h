@@ -46,9 +46,13 @@ int sinkattn_abi_version(void);
  * the external kernel consumed the bool mask directly; here it is turned once into
  *   counts[B*H*nqb]          number of listed key blocks per row,
  *   idx[B*H*nqb*nkb]         the listed key blocks of row r in idx[r*nkb .. r*nkb+counts[r]),
- *   order[B*H*nqb]           rows sorted by descending count (longest-first launch order).
+ *   order[slots]             launch order, slots = sinkattn_block_sparse_order_slots():
+ *                            work-group i (on XCD i % 8) runs row order[i] (-1: none);
+ *                            XCD x gets the q-blocks qb = x mod 8 of every (b, h), head
+ *                            by head, longest first within a head.
  * `mask` is uint8/bool [B,H,nqb,nkb] with element strides mask_strides[4].
  * ---------------------------------------------------------------------------------- */
+int64_t sinkattn_block_sparse_order_slots(int64_t B, int64_t H, int64_t nqb);
 int sinkattn_block_sparse_plan(const uint8_t* mask, const int64_t mask_strides[4],
                                int64_t B, int64_t H, int64_t nqb, int64_t nkb,
                                int32_t* counts, int32_t* idx, int32_t* order,
@@ -65,7 +69,8 @@ int sinkattn_block_sparse_plan(const uint8_t* mask, const int64_t mask_strides[4
  * above), dtype one of sinkattn_dtype (f32 operands are rounded to bf16 for the matrix
  * cores; accumulation and softmax are fp32).  lse is fp32 [B,H,Nq] contiguous, or NULL.
  * A row with no listed key block gets out = 0 and lse = +inf.
- * counts/idx/order come from sinkattn_block_sparse_plan (order may be NULL).
+ * counts/idx/order come from sinkattn_block_sparse_plan (order may be NULL: one
+ * work-group per row in row order).
  * D must be 64 or 128.
  * ---------------------------------------------------------------------------------- */
 int sinkattn_block_sparse_fwd(const void* q, const void* k, const void* v, int dtype,

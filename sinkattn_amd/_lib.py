@@ -26,6 +26,7 @@ _c_i64_4 = ctypes.c_int64 * 4
 SIGNATURES = {
     "sinkattn_last_error": (ctypes.c_char_p, []),
     "sinkattn_abi_version": (ctypes.c_int, []),
+    "sinkattn_block_sparse_order_slots": (ctypes.c_int64, [_c_i64, _c_i64, _c_i64]),
     "sinkattn_block_sparse_plan": (
         ctypes.c_int,
         [_c_p, _c_i64_4, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p],

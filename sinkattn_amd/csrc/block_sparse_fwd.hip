@@ -37,6 +37,7 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_kernel(FwdArgs a) {
   const int hl = lane >> 5, l32 = lane & 31;
 
   const int item = a.order ? a.order[blockIdx.x] : (int)blockIdx.x;
+  if (item < 0) return;
   const int bh = item / a.nqb;
   const int qb = item - bh * a.nqb;
   const int b = bh / a.H, h = bh - b * a.H;
@@ -174,11 +175,12 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
   __shared__ u32x4 lds_v[2048];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, l32 = lane & 31;
   // Work-item values are uniform: keep them in scalar registers so the list walk uses
   // scalar loads and never enters the vector-memory counter the DMA waits rely on.
   const int item = __builtin_amdgcn_readfirstlane(a.order ? a.order[blockIdx.x] : (int)blockIdx.x);
+  if (item < 0) return;
   const int bh = item / a.nqb;
   const int qb = item - bh * a.nqb;
   const int b = bh / a.H, h = bh - b * a.H;
@@ -377,6 +379,7 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_f32_kernel(FwdArgs a) {
   const int lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, l32 = lane & 31;
   const int item = a.order ? a.order[blockIdx.x] : (int)blockIdx.x;
+  if (item < 0) return;
   const int bh = item / a.nqb;
   const int qb = item - bh * a.nqb;
   const int b = bh / a.H, h = bh - b * a.H;
@@ -547,27 +550,33 @@ __global__ __launch_bounds__(256) void plan_rows_kernel(PlanArgs a) {
   if (lane == 0) a.counts[row] = base;
 }
 
-// Single work-group counting sort of rows by descending count.
-__global__ __launch_bounds__(1024) void plan_order_kernel(PlanArgs a) {
-  extern __shared__ int hist[];  // nkb + 1 bins
-  const int tid = threadIdx.x;
-  for (int i = tid; i <= a.nkb; i += blockDim.x) hist[i] = 0;
-  __syncthreads();
-  for (int i = tid; i < a.rows; i += blockDim.x) atomicAdd(&hist[a.counts[i]], 1);
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int c = a.nkb; c >= 0; --c) {
-      const int n = hist[c];
-      hist[c] = run;
-      run += n;
+// Launch order.  Work-group i runs on XCD i % 8 and each XCD has its own L2, so the
+// order gives XCD x the q-blocks qb = x (mod 8) of every (b, h), head by head: the
+// work-groups resident on one XCD at a time share one or two heads' K/V, which they
+// walk in the same ascending key-block order, and every XCD gets the same share of
+// every head (balanced whatever the per-head densities).  Within one (b, h, x) slice
+// the q-blocks run longest-first.  Slots past the end of a shorter slice hold -1.
+__global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
+  const int slices = (a.nqb + kXcds - 1) / kXcds;  // slots per (b, h) per XCD
+  const int total = a.rows / a.nqb * slices * kXcds;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) a.order[i] = -1;
+  __syncthreads();  // launched as a single work-group: the fill precedes every placement
+  for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
+    const int bh = row / a.nqb, qb = row - bh * a.nqb;
+    const int x = qb % kXcds;
+    const int c = a.counts[row];
+    int rank = 0;
+    for (int q2 = x; q2 < a.nqb; q2 += kXcds) {
+      const int c2 = a.counts[bh * a.nqb + q2];
+      rank += (c2 > c) || (c2 == c && q2 < qb);
     }
+    a.order[(bh * slices + rank) * kXcds + x] = row;
   }
-  __syncthreads();
-  for (int i = tid; i < a.rows; i += blockDim.x) {
-    const int pos = atomicAdd(&hist[a.counts[i]], 1);
-    a.order[pos] = i;
-  }
+}
+
+int plan_order_slots(int rows, int nqb) {
+  if (rows == 0 || nqb == 0) return 0;
+  return rows / nqb * ((nqb + kXcds - 1) / kXcds) * kXcds;
 }
 
 hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream) {
@@ -575,13 +584,18 @@ hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream) {
   plan_rows_kernel<<<(a.rows + 3) / 4, 256, 0, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.order == nullptr) return e;
-  plan_order_kernel<<<1, 1024, (a.nkb + 1) * sizeof(int), stream>>>(a);
+  plan_order_kernel<<<1, 256, 0, stream>>>(a);
   return hipGetLastError();
+}
+
+static int fwd_grid(const FwdArgs& a) {
+  const int rows = a.B * a.H * a.nqb;
+  return a.order ? plan_order_slots(rows, a.nqb) : rows;
 }
 
 template <int IT, int CT>
 static hipError_t launch_fwd_dt(const FwdArgs& a, int D, hipStream_t stream) {
-  const int grid = (int)(a.B * a.H * a.nqb);
+  const int grid = fwd_grid(a);
   if (D == 128)
     block_sparse_fwd_d128_kernel<CT><<<grid, 256, 0, stream>>>(a);
   else
@@ -595,7 +609,7 @@ hipError_t launch_block_sparse_fwd(const FwdArgs& a, int dtype, int D, hipStream
     case kBF16: return launch_fwd_dt<kBF16, kBF16>(a, D, stream);
     case kF16: return launch_fwd_dt<kF16, kF16>(a, D, stream);
     default: {
-      const int grid = (int)(a.B * a.H * a.nqb);
+      const int grid = fwd_grid(a);
       if (D == 128)
         block_sparse_fwd_f32_kernel<128><<<grid, 256, 0, stream>>>(a);
       else

@@ -57,6 +57,11 @@ const char* sinkattn_last_error(void) { return g_last_error.c_str(); }
 
 int sinkattn_abi_version(void) { return 1; }
 
+int64_t sinkattn_block_sparse_order_slots(int64_t B, int64_t H, int64_t nqb) {
+  if (B <= 0 || H <= 0 || nqb <= 0 || B * H * nqb > kMaxInt) return 0;
+  return sa::plan_order_slots((int)(B * H * nqb), (int)nqb);
+}
+
 int sinkattn_block_sparse_plan(const uint8_t* mask, const int64_t mask_strides[4], int64_t B,
                                int64_t H, int64_t nqb, int64_t nkb, int32_t* counts,
                                int32_t* idx, int32_t* order, void* stream) {

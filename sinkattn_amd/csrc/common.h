@@ -25,18 +25,19 @@ __device__ __forceinline__ float pos_inf() { return __builtin_inff(); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// fp32 -> 16-bit float bits, round to nearest even (hardware v_cvt_pk_bf16_f32 / cvt_f16).
+// Two fp32 -> packed 16-bit floats (lo in bits 0-15), round to nearest even: one
+// v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 template <int CT>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi);
 template <>
 __device__ __forceinline__ uint32_t pack2<kBF16>(float lo, float hi) {
-  __bf16 a = (__bf16)lo, b = (__bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 template <>
 __device__ __forceinline__ uint32_t pack2<kF16>(float lo, float hi) {
-  _Float16 a = (_Float16)lo, b = (_Float16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {

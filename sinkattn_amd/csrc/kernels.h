@@ -55,6 +55,8 @@ struct MaskArgs {
   uint8_t* ws_flags;  // [H*nq] workspace
 };
 
+constexpr int kXcds = 8;  // gfx950: work-group i is dispatched to XCD i % 8
+int plan_order_slots(int rows, int nqb);
 hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream);
 hipError_t launch_block_sparse_fwd(const FwdArgs& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);

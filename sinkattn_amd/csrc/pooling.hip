@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256, 3) void block_mass_persistent_kernel(PoolArgs 
   __shared__ u32x4 lds_k[2048];
   __shared__ float row_inv[128];
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, l32 = lane & 31;
   const int nkb = a.nkb;
   float* ws = a.ws + (size_t)blockIdx.x * (size_t)nkb * 128;

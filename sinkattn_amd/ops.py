@@ -46,7 +46,7 @@ class BlockSparsePlan:
 
     counts: torch.Tensor  # int32 [B*H*nqb]
     idx: torch.Tensor  # int32 [B*H*nqb*nkb]
-    order: torch.Tensor  # int32 [B*H*nqb], rows by descending count
+    order: torch.Tensor  # int32 launch slots (XCD-aware; -1 = empty slot)
     shape: Tuple[int, int, int, int]  # B, H, nqb, nkb
 
     @property
@@ -65,10 +65,11 @@ def block_sparse_plan(block_mask: torch.Tensor) -> BlockSparsePlan:
     B, H, nqb, nkb = (int(x) for x in m.shape)
     dev = m.device
     rows = B * H * nqb
+    L = _lib.lib()
     counts = torch.empty(rows, dtype=torch.int32, device=dev)
     idx = torch.empty(rows * nkb, dtype=torch.int32, device=dev)
-    order = torch.empty(rows, dtype=torch.int32, device=dev)
-    L = _lib.lib()
+    order = torch.empty(max(int(L.sinkattn_block_sparse_order_slots(B, H, nqb)), 1), dtype=torch.int32,
+                        device=dev)
     with torch.cuda.device(dev):
         st = _lib.strides4(m)
         _lib.check(

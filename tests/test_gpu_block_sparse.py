@@ -136,8 +136,18 @@ def test_plan_lists_and_order():
         assert counts[r].item() == want.numel()
         assert torch.equal(idx[r, : want.numel()], want)
     order = plan.order.cpu()
-    assert torch.equal(order.sort().values, torch.arange(flat.shape[0], dtype=torch.int32))
-    assert (counts[order][:-1] >= counts[order][1:]).all()
+    real = order[order >= 0]
+    assert torch.equal(real.sort().values, torch.arange(flat.shape[0], dtype=torch.int32))
+    # slot i runs on XCD i % 8: XCD x holds the q-blocks qb = x mod 8, longest first per head
+    nqb = 7
+    for i, row in enumerate(order.tolist()):
+        if row >= 0:
+            assert (row % nqb) % 8 == i % 8
+    for bh in range(6):
+        for x in range(8):
+            slot_rows = [r for i, r in enumerate(order.tolist()) if r >= 0 and r // nqb == bh and i % 8 == x]
+            cs = [int(counts[r]) for r in slot_rows]
+            assert cs == sorted(cs, reverse=True)
 
 
 def test_bad_mask_shape_raises():
