@@ -14,7 +14,7 @@ from typing import Optional, Sequence
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "libsinkattn.so"
+LIB_PATH = Path(os.environ.get("SINKATTN_LIB", Path(__file__).resolve().parent / "libsinkattn.so"))
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 

@@ -163,8 +163,8 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_kernel(FwdArgs a) {
 // D = 128, bf16/f16: K and V tiles go global -> LDS by buffer DMA (no staging
 // registers; rows >= Nk read as zero through the buffer bounds), and V^T is read from
 // the row-major V tile with the gfx950 transpose read ds_read_b64_tr_b16.  K and V are
-// double-staged against each other: K(i+1) streams in while softmax(i) and PV(i) run,
-// V(i+1) while S(i+1) runs.  LDS layout: 128 rows x 16 chunks of 16 bytes per tile,
+// staged against each other: K(i+1) streams in while softmax(i) and PV(i) run, V(i+1)
+// while S(i+1) runs, with two work-group barriers per tile.  LDS layout: 128 rows x 16 chunks of 16 bytes per tile,
 // physical chunk = logical ^ (row & 15) for K and logical ^ (4 * (row & 3)) for V, which
 // keeps the 16-lane K reads and the 32-lane transpose reads on distinct banks.
 // ------------------------------------------------------------------------------------
@@ -248,27 +248,46 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
   float l_run = 0.f;
   const float c = a.scale * kLog2e;
 
+  // Two barriers per tile.  B1 (after S): every wave is done reading K(it) and V(it)
+  // has landed -> K(it+1) may stream in.  B2 (after PV): every wave is done reading V(it)
+  // and K(it+1) has landed -> V(it+1) may stream in.
   if (cnt > 0) {
     const int kb0 = list[0];
     issue_k(kb0);
     issue_v(kb0);
+    // Drain both: waiting only for K(0) here leaves the compiler unable to prove at the
+    // loop head that V's copies do not alias the K reads, and it then waits there on
+    // every tile.
+    drain_then_barrier();
   }
   for (int it = 0; it < cnt; ++it) {
     const int key0 = list[it] * 128;
     const bool next = it + 1 < cnt;
-    wait_vmcnt<8>();  // this wave's K(it) has landed (V(it) may still be in flight)
-    __builtin_amdgcn_s_barrier();
     f32x16 s[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) s[t] = f32x16{};
+    {
+      // Reads for k-step ds+1 are issued between the MFMAs of k-step ds, one read after
+      // each MFMA; the scheduling groups pin that order so no MFMA waits on the read
+      // issued just before it.
+      u32x4 kr[2][4];
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds)
+      for (int t = 0; t < 4; ++t) kr[0][t] = *(SA_LDS const u32x4*)(lk + ka[0] + t * 8192);
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const u32x4 av = *(SA_LDS const u32x4*)(lk + ka[ds] + t * 8192);
-        s[t] = mfma32x32x16<CT>(av, qf[ds], s[t]);
+      for (int ds = 0; ds < DS; ++ds) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          s[t] = mfma32x32x16<CT>(kr[ds & 1][t], qf[ds], s[t]);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (ds + 1 < DS) {
+            kr[(ds + 1) & 1][t] = *(SA_LDS const u32x4*)(lk + ka[ds + 1] + t * 8192);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+        }
       }
-    __builtin_amdgcn_s_barrier();  // every wave is done reading K(it)
+    }
+    drain_then_barrier();  // B1: V(it) has landed, K(it) reads are done
     const int kb_next = next ? list[it + 1] : 0;
     if (next) issue_k(kb_next);
 
@@ -308,25 +327,37 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
         }
     l_run += lsum;
 
-    if (next)
-      wait_vmcnt<8>();  // V(it) landed; K(it+1) may be in flight
-    else
-      wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
+    // Raised issue priority over the PV MFMAs: the other wave on this SIMD (another
+    // work-group) then fills the VALU slots with its softmax instead of competing
+    // with these MFMAs for issue.
+    __builtin_amdgcn_s_setprio(1);
+    {
+      // V^T operands one (t, u) step ahead: 4 d-tiles per step.
+      auto vread = [&](int dt, int t, int u) -> u32x4 {
+        const uint32_t off = t * 8192 + u * 4096;
+        const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][0] + off));
+        const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][1] + off));
+        const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
+        return u32x4{y0[0], y0[1], y1[0], y1[1]};
+      };
+      u32x4 cur[DT], nxt[DT];
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt) cur[dt] = vread(dt, 0, 0);
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int step = 0; step < 8; ++step) {
+        const int t = step >> 1, u = step & 1;
+        if (step + 1 < 8) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const uint32_t off = t * 8192 + u * 4096;
-          const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][0] + off));
-          const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][1] + off));
-          const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
-          const u32x4 av = u32x4{y0[0], y0[1], y1[0], y1[1]};
-          o[dt] = mfma32x32x16<CT>(av, p[t][u], o[dt]);
+          for (int dt = 0; dt < DT; ++dt) nxt[dt] = vread(dt, (step + 1) >> 1, (step + 1) & 1);
         }
-    __builtin_amdgcn_s_barrier();  // every wave is done reading V(it)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] = mfma32x32x16<CT>(cur[dt], p[t][u], o[dt]);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) cur[dt] = nxt[dt];
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    drain_then_barrier();  // B2: K(it+1) has landed, V(it) reads are done
     if (next) issue_v(kb_next);
   }
 

@@ -148,6 +148,14 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Work-group barrier after this wave's buffer->LDS copies have landed and its own LDS
+// reads have returned, so a buffer may be refilled by any wave right after it.
+// (__syncthreads would do the same plus a full fence; this keeps it to the counters.)
+__device__ __forceinline__ void drain_then_barrier() {
+  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0 << 8));  // vmcnt(0) expcnt(7) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+}
+
 #define SA_LDS __attribute__((address_space(3)))
 #define SA_CONST __attribute__((address_space(4)))
 
