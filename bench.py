@@ -30,6 +30,19 @@ import time
 MFMA_BF16_PEAK_TFLOPS = 2516.6
 HBM_PEAK_GBS = 8000.0
 
+# HBM traffic per launch at the default workload (--density 0.20, the seeds below),
+# from rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (KiB per dispatch) scaled by what
+# the same counters read for a 1 GiB device copy in the same run (FETCH_SIZE reads
+# 0.5 GiB for it -> x2.0, WRITE_SIZE reads 1 GiB -> x1.0).  Summaries with the commands:
+# profiles/block_sparse_fwd_wan_c2.md and profiles/block_mass_pool_wan_c2.md.
+FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
+TRAFFIC_KIB = {"fa": (5231235.0, 200742.0), "pool": (1292967.0, 792576.0)}
+
+
+def traffic_bytes(kind):
+    fetch, write = TRAFFIC_KIB[kind]
+    return (fetch * FETCH_SCALE + write * WRITE_SCALE) * 1024.0
+
 
 def _parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -39,8 +52,8 @@ def _parse():
     p.add_argument("--density", type=float, default=0.20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true", help="skip dense/pooling/mask timings")
-    p.add_argument("--cpu-sample-qblocks", type=int, default=1024,
-                   help="q-blocks of the layer the CPU baseline times (1024 = heads 0-3 of batch 0)")
+    p.add_argument("--cpu-sample-qblocks", type=int, default=0,
+                   help="q-blocks of the layer the CPU baseline times (0 = the whole layer, 6144)")
     p.add_argument("--only", choices=["all", "fa", "pool", "mask"], default="all",
                    help="profiling aid: run just one kernel family (no JSON line unless 'all')")
     p.add_argument("--copy-mb", type=int, default=0,
@@ -82,35 +95,55 @@ def tile_flops(torch, mask, Nq, Nk, D, block=128):
     return float(4.0 * D * torch.einsum("bhqk,q,k->", m, rows, keys))
 
 
-def time_fn(torch, fn, steps, warmup):
+def time_fn(torch, fn, steps, warmup, per_launch=False):
+    """Mean ms per call over `steps` calls after `warmup` untimed ones, bracketed by
+    device synchronisation.  The library enqueues on torch's current stream, so events
+    recorded there bracket the kernels.  With per_launch, an event pair also brackets
+    every call and the mean of those (the kernel's average launch duration) is returned
+    as a second value."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(steps)] if per_launch else None
     s.record()
-    for _ in range(steps):
+    for i in range(steps):
+        if marks:
+            marks[i][0].record()
         fn()
+        if marks:
+            marks[i][1].record()
     e.record()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / steps
+    total = s.elapsed_time(e) / steps
+    if per_launch:
+        return total, sum(a.elapsed_time(b) for a, b in marks) / steps
+    return total
 
 
 def cpu_baseline(torch, q, k, v, mask, n_qblocks, total_flops_layer):
-    """Oracle fp32 block-gather masked softmax on the host for a sample of q-blocks of
-    (b, h) = (0, 0); reported as the full-layer rate extrapolated from the sample."""
+    """The oracle's fp32 block-gather masked softmax on the host (torch CPU, all of its
+    threads), over the first `n_qblocks` q-blocks of the layer in (b, h, qb) order, or
+    the whole layer for 0.  Only the per-q-block compute is timed (not the device->host
+    copies); a partial sample is reported with the full-layer time extrapolated."""
     from oracle import torch_ref  # noqa: F401  (the checker package; timed here as the CPU baseline)
 
-    N, D = int(q.shape[2]), int(q.shape[3])
+    B, H, N, D = (int(x) for x in q.shape)
     nqb = int(mask.shape[2])
+    total_q = B * H * nqb
+    n_qblocks = total_q if n_qblocks <= 0 else min(n_qblocks, total_q)
     scale = 1.0 / math.sqrt(D)
-    heads = max(1, min(int(q.shape[1]), -(-n_qblocks // nqb)))
     flops = 0.0
     done = 0
     dt = 0.0
-    for h in range(heads):
-        qs, ks, vs = (t[0, h].float().cpu() for t in (q, k, v))
-        m = mask[0, h].cpu()
+    for bh in range(B * H):
+        if done >= n_qblocks:
+            break
+        b, h = divmod(bh, H)
+        qs, ks, vs = (t[b, h].float().cpu() for t in (q, k, v))
+        m = mask[b, h].cpu()
         t0 = time.perf_counter()
         for qb in range(nqb):
             if done >= n_qblocks:
@@ -124,16 +157,17 @@ def cpu_baseline(torch, q, k, v, mask, n_qblocks, total_flops_layer):
             flops += 4.0 * (rows.stop - rows.start) * keys.numel() * D
             done += 1
         dt += time.perf_counter() - t0
-    sample = range(done)
     rate = flops / dt
+    whole = done == total_q
     return {
         "value": rate / 1e12,
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{len(sample)} q-blocks (batch 0, heads 0-{heads - 1}) of the config-2 layer, fp32 torch on CPU "
-                  f"({dt:.1f} s); full layer extrapolated: {total_flops_layer / rate * 1e3:.0f} ms",
-        "ms_per_layer_extrapolated": total_flops_layer / rate * 1e3,
+        "sample": (f"{done} of {total_q} q-blocks of the config-2 layer"
+                   + (" (whole layer)" if whole else " (full layer extrapolated)")
+                   + f", fp32 torch block-gather softmax on CPU, {dt:.1f} s"),
+        "ms_per_layer": round(total_flops_layer / rate * 1e3, 1),
         "os_cpu_count": os.cpu_count(),
     }
 
@@ -176,9 +210,13 @@ def main():
         print(f"ran {args.only} x{args.warmup + args.steps}")
         return
 
-    ms = time_fn(torch, step, args.steps, args.warmup)
+    ms, kms = time_fn(torch, step, args.steps, args.warmup, per_launch=True)
     tflops = flops / (ms * 1e-3) / 1e12
+    ktflops = flops / (kms * 1e-3) / 1e12
     density = float(mask.float().mean())
+    default_workload = abs(args.density - 0.20) < 1e-9
+    # algorithmic bytes of one launch: Q, K, V read once, O written (bf16), LSE (fp32)
+    fa_bytes = 4 * q.numel() * 2 + B * H * N * 4
 
     out = {
         "metric": "ms/layer + effective TFLOP/s sparse attn @Wan N=32760; pooling HBM GB/s",
@@ -196,10 +234,12 @@ def main():
         "config": {"workload": "wan2.1-1.3b layer block-sparse attention (config 2)", "batch": B,
                    "heads": H, "seq_len": N, "head_dim": D, "block": 128,
                    "mask_density": round(density, 4), "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "traffic": None, "kernel": "block_sparse_fwd_kernel<bf16,bf16,128>",
-                     "flops_per_launch": flops},
+        "roofline": {"bound": "mfma", "achieved": round(ktflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(ktflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": traffic_bytes("fa") if default_workload else None,
+                     "kernel": "sa::block_sparse_fwd_d128_kernel<0> (bf16)",
+                     "flops_per_launch": flops, "kernel_ms": round(kms, 4),
+                     "algorithmic_bytes": fa_bytes},
         "ms_per_layer": round(ms, 4),
         "dense_equivalent_tflops": round(dense_flops / (ms * 1e-3) / 1e12, 2),
     }
@@ -217,7 +257,9 @@ def main():
         out["pooling"] = {"ms": round(pms, 3), "tflops": round(pool_flops / (pms * 1e-3) / 1e12, 2),
                           "hbm_gbs_algorithmic": round(pool_bytes / (pms * 1e-3) / 1e9, 2),
                           "hbm_frac": round(pool_bytes / (pms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5),
-                          "mfma_frac": round(pool_flops / (pms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+                          "mfma_frac": round(pool_flops / (pms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                          "traffic": traffic_bytes("pool"),
+                          "kernel": "sa::block_mass_persistent_kernel<0> (bf16)"}
         scores = torch.rand(H, 256, 256, device=dev)
         scores = scores / scores.sum(-1, keepdim=True)
         mus = time_fn(torch, lambda: ops.coverage_mask(scores, 0.85, True), 10, 2) * 1e3
