@@ -277,3 +277,32 @@ def mix(sink_out, sink_lse, dyn_out, dyn_lse, sample_gap: int):
     es, ed = torch.exp(ws - mx), torch.exp(wd - mx)
     a = es / (es + ed)
     return sink_out * a + dyn_out * (1.0 - a)
+
+
+# ---------------------------------------------------------------------------------------
+# sinkattention/sparse_attention.py:79-115  (_pad_to_multiple, _mean_pool_sequence,
+# _mean_pool_sequence_preserve_prefix): the compensation branch's K/V pooling.
+# ---------------------------------------------------------------------------------------
+def mean_pool_tokens(x: torch.Tensor, gap: int, prefix: int = 0) -> torch.Tensor:
+    """fp32 on CPU.  Rows [0, prefix) of dim 2 are kept as they are; the remaining rows
+    are taken in groups of ``gap`` consecutive rows and each group becomes its mean; a
+    short last group counts its last row again for every missing row (replicate
+    padding).  ``gap`` <= 1 returns the input; ``prefix`` >= rows returns the input."""
+    x = x.detach().cpu().float()
+    n = x.size(2)
+    if gap <= 1:
+        return x
+    prefix = min(max(int(prefix), 0), n)
+    if prefix >= n:
+        return x
+    body = x[:, :, prefix:]
+    m = body.size(2)
+    groups = []
+    for g0 in range(0, m, gap):
+        rows = body[:, :, g0:min(g0 + gap, m)]
+        missing = gap - rows.size(2)
+        total = rows.sum(dim=2)
+        if missing:
+            total = total + missing * body[:, :, m - 1]
+        groups.append(total / gap)
+    return torch.cat([x[:, :, :prefix], torch.stack(groups, dim=2)], dim=2)
