@@ -9,7 +9,7 @@ Contents
 torch_ref   CPU torch restatements of the reference functions, each citing the
             reference file:line it follows (exact block mass, max-pool closed form,
             mean-pooled scores, coverage mask, required mask, dense masked softmax
-            attention with LSE, LSE mixing).
+            attention with LSE, LSE mixing, the compensation branch's K/V mean pooling).
 c_ref       ctypes loader of oracle/_build/liboracle.so: the plain-C coverage-mask
             restatement (ATen fp32 sum order, fp64 cumsum, libstdc++ std::sort
             emulation) and the real libstdc++ std::sort.
@@ -24,6 +24,11 @@ How each function is pinned (tests/test_oracle_*.py):
                        minimal-k definition on small rows, invariants and special cases
   dense attention      SDPA on a full mask, block-local attention on a diagonal mask,
                        logsumexp identity
+  LSE mixing           equals attention over the union of both key sets with the pooled
+                       keys counted sample_gap times (fp64 identity); plain average at
+                       gap 1 and equal LSEs
+  K/V mean pooling     ramp and constant closed forms, replicate-padded last group,
+                       prefix rows untouched, identities at gap 1 / prefix >= N
 Parity unpinned: the bf16 bit pattern of the reference Triton max-pool kernel
 (``attn_with_pooling``) beyond "within bf16 rounding", and its ragged-N behaviour
 (undefined in the reference).
