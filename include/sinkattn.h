@@ -83,6 +83,68 @@ int sinkattn_block_sparse_fwd(const void* q, const void* k, const void* v, int d
                               float softmax_scale, void* stream);
 
 /* ------------------------------------------------------------------------------------
+ * Block-sparse forward fused with the compensation branch ("pooled_kv" dynamic mode with
+ * adaptive mixing).
+ *
+ * Replaces the sparse call, the attention over the pooled K/V and `_mix_attention_outputs`
+ * of `WanSinkSparseInnerAttention.forward` (wanx/runtime/sink_sparse_wan.py:194-265;
+ * sinkattention/sparse_attention.py:898-919) and of the Z-Image image rows
+ * (zimg/runtime/sink_sparse_zimage.py:553-592).  The reference computes
+ *     out = a*out_s + (1-a)*out_d,  a = exp(lse_s) / (exp(lse_s) + gap*exp(lse_d)),
+ * which equals attention over the listed keys plus every pooled key counted `gap`
+ * times.  Here the q-blocks qb < comp_qblocks attend, after their listed tiles, every
+ * key of kd/vd [B,H,Nd,D] (BHSD-addressed, row strides equal to k's/v's) with log_gap =
+ * ln(gap) added to the scaled logits, in one online softmax; other q-blocks are plain
+ * block-sparse rows.  lse (optional) is the LSE of that union.  bf16/f16, D = 128.
+ * ---------------------------------------------------------------------------------- */
+int sinkattn_block_sparse_fwd_comp(const void* q, const void* k, const void* v, int dtype,
+                                   int64_t B, int64_t H, int64_t Nq, int64_t Nk, int64_t D,
+                                   const int64_t q_strides[4], const int64_t k_strides[4],
+                                   const int64_t v_strides[4],
+                                   const void* kd, const void* vd,
+                                   const int64_t kd_strides[4], const int64_t vd_strides[4],
+                                   int64_t Nd, int64_t comp_qblocks, float log_gap,
+                                   void* out, const int64_t out_strides[4], float* lse,
+                                   const int32_t* counts, const int32_t* idx,
+                                   const int32_t* order, int64_t nqb, int64_t nkb,
+                                   float softmax_scale, void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Token mean pooling of the compensation branch.
+ *
+ * Replaces `_mean_pool_sequence_preserve_prefix` / `_mean_pool_sequence` /
+ * `_pad_to_multiple` (sinkattention/sparse_attention.py:79-115): rows [0, prefix) of x
+ * are copied; the remaining rows are averaged in groups of `gap` (a short last group
+ * repeats row N-1, i.e. replicate padding).  fp32 sums, times fp32(1/gap), one rounding
+ * to the dtype.  gap == 1 or prefix >= N copy x.  out has
+ * sinkattn_mean_pool_tokens_rows(N, prefix, gap) rows.  D*elem_size must be a power of
+ * two between 16 and 4096 bytes.
+ * ---------------------------------------------------------------------------------- */
+int64_t sinkattn_mean_pool_tokens_rows(int64_t N, int64_t prefix, int64_t gap);
+int sinkattn_mean_pool_tokens(const void* x, int dtype, int64_t B, int64_t H, int64_t N,
+                              int64_t D, const int64_t x_strides[4], int64_t prefix,
+                              int64_t gap, void* out, const int64_t out_strides[4],
+                              void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * LSE mix of two attention outputs.
+ *
+ * Replaces `_mix_attention_outputs` (sinkattention/sparse_attention.py:898-919) for
+ * callers that run the two branches separately, with the reference's rounding: each of
+ * its torch ops on q.dtype tensors is one fp32 operation rounded to the dtype:
+ *     wd = dyn_lse + log_gap; mx = max(sink_lse, wd); es = exp(sink_lse - mx);
+ *     ed = exp(wd - mx); a = es / (es + ed); out = sink*a + dyn*(1 - a)
+ * log_gap is the caller's q.dtype value of log(gap).  Outputs/inputs BHSD-addressed
+ * [B,H,N,D]; the LSEs are [B,H,N] addressed by 3 strides, same dtype as the outputs.
+ * ---------------------------------------------------------------------------------- */
+int sinkattn_lse_mix(const void* sink_out, const int64_t sink_strides[4],
+                     const void* sink_lse, const int64_t sink_lse_strides[3],
+                     const void* dyn_out, const int64_t dyn_strides[4],
+                     const void* dyn_lse, const int64_t dyn_lse_strides[3], int dtype,
+                     int64_t B, int64_t H, int64_t N, int64_t D, float log_gap,
+                     void* out, const int64_t out_strides[4], void* stream);
+
+/* ------------------------------------------------------------------------------------
  * Exact block-mass pooling ("exact" pooling mode).
  *
  * Replaces `_compute_exact_block_mass_scores` (sinkattention/sparse_attention.py:145-227):

@@ -21,6 +21,7 @@ DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 _c_i64 = ctypes.c_int64
 _c_p = ctypes.c_void_p
 _c_i64_4 = ctypes.c_int64 * 4
+_c_i64_3 = ctypes.c_int64 * 3
 
 # name -> (restype, argtypes); must match include/sinkattn.h
 SIGNATURES = {
@@ -36,6 +37,22 @@ SIGNATURES = {
         [_c_p, _c_p, _c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_i64_4, _c_i64_4, _c_i64_4, _c_p, _c_i64_4, _c_p, _c_p, _c_p, _c_p,
          _c_i64, _c_i64, ctypes.c_float, _c_p],
+    ),
+    "sinkattn_block_sparse_fwd_comp": (
+        ctypes.c_int,
+        [_c_p, _c_p, _c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64_4, _c_i64_4, _c_i64_4, _c_p, _c_p, _c_i64_4, _c_i64_4, _c_i64, _c_i64, ctypes.c_float,
+         _c_p, _c_i64_4, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, ctypes.c_float, _c_p],
+    ),
+    "sinkattn_mean_pool_tokens_rows": (ctypes.c_int64, [_c_i64, _c_i64, _c_i64]),
+    "sinkattn_mean_pool_tokens": (
+        ctypes.c_int,
+        [_c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64_4, _c_i64, _c_i64, _c_p, _c_i64_4, _c_p],
+    ),
+    "sinkattn_lse_mix": (
+        ctypes.c_int,
+        [_c_p, _c_i64_4, _c_p, _c_i64_3, _c_p, _c_i64_4, _c_p, _c_i64_3, ctypes.c_int, _c_i64, _c_i64,
+         _c_i64, _c_i64, ctypes.c_float, _c_p, _c_i64_4, _c_p],
     ),
     "sinkattn_block_mass_pool_workspace_bytes": (
         ctypes.c_size_t, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int],
@@ -114,6 +131,11 @@ def stream_ptr(device: torch.device) -> int:
 def strides4(t: torch.Tensor) -> "ctypes.Array":
     s: Sequence[int] = t.stride()
     return _c_i64_4(*[int(x) for x in s])
+
+
+def strides3(t: torch.Tensor) -> "ctypes.Array":
+    s: Sequence[int] = t.stride()
+    return _c_i64_3(*[int(x) for x in s])
 
 
 def ptr(t: Optional[torch.Tensor]) -> Optional[int]:

@@ -24,6 +24,7 @@ SOURCES = [
     "block_sparse_fwd.hip",
     "pooling.hip",
     "coverage_mask.hip",
+    "compensation.hip",
     "capi.cpp",
 ]
 

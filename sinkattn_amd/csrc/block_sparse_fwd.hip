@@ -188,11 +188,19 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
   // The plan is read-only for the kernel's lifetime: read it through the constant
   // address space so the list walk compiles to scalar loads.
   const SA_CONST int32_t* list = (const SA_CONST int32_t*)(a.idx + (int64_t)item * a.nkb);
+  // Compensation tiles: after its listed tiles, a q-block below comp_qblocks attends every
+  // 128-key tile of kd/vd (same row strides as k/v) with comp_bias added to its logits.
+  const int ntot = cnt + (qb < a.comp_qblocks ? (a.Nd + 127) >> 7 : 0);
 
   const char* qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * 2;
   const char* kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)h * a.ks[1]) * 2;
   const char* vbase = (const char*)a.v + ((int64_t)b * a.vs[0] + (int64_t)h * a.vs[1]) * 2;
+  const char* kdbase = (const char*)a.kd + ((int64_t)b * a.kds[0] + (int64_t)h * a.kds[1]) * 2;
+  const char* vdbase = (const char*)a.vd + ((int64_t)b * a.vds[0] + (int64_t)h * a.vds[1]) * 2;
   const uint32_t kstride = (uint32_t)a.ks[2] * 2, vstride = (uint32_t)a.vs[2] * 2;
+  // Tile `it` of the walk: first key, valid key count, and whether it is a compensation tile.
+  auto tile_key0 = [&](int it) { return it < cnt ? list[it] * 128 : (it - cnt) * 128; };
+  auto tile_limit = [&](int it) { return it < cnt ? a.Nk : a.Nd; };
 
   const int qrow = qb * 128 + wave * 32 + l32;
   u32x4 qf[DS];
@@ -226,16 +234,18 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
   SA_LDS char* lk = (SA_LDS char*)lds_k;
   SA_LDS char* lv = (SA_LDS char*)lds_v;
 
-  auto issue_k = [&](int kb) {
-    const int key0 = kb * 128;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(kbase + (int64_t)key0 * kstride, (uint32_t)(a.Nk - key0) * kstride);
+  auto issue_k = [&](int it) {
+    const int key0 = tile_key0(it);
+    const char* base = (it < cnt ? kbase : kdbase) + (int64_t)key0 * kstride;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(tile_limit(it) - key0) * kstride);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       dma16(rs, (SA_LDS void*)(lk + (256 * j + 64 * wave) * 16), k_off + (uint32_t)j * 16u * kstride);
   };
-  auto issue_v = [&](int kb) {
-    const int key0 = kb * 128;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(vbase + (int64_t)key0 * vstride, (uint32_t)(a.Nk - key0) * vstride);
+  auto issue_v = [&](int it) {
+    const int key0 = tile_key0(it);
+    const char* base = (it < cnt ? vbase : vdbase) + (int64_t)key0 * vstride;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(tile_limit(it) - key0) * vstride);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       dma16(rs, (SA_LDS void*)(lv + (256 * j + 64 * wave) * 16), v_off + (uint32_t)j * 16u * vstride);
@@ -251,18 +261,19 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
   // Two barriers per tile.  B1 (after S): every wave is done reading K(it) and V(it)
   // has landed -> K(it+1) may stream in.  B2 (after PV): every wave is done reading V(it)
   // and K(it+1) has landed -> V(it+1) may stream in.
-  if (cnt > 0) {
-    const int kb0 = list[0];
-    issue_k(kb0);
-    issue_v(kb0);
+  if (ntot > 0) {
+    issue_k(0);
+    issue_v(0);
     // Drain both: waiting only for K(0) here leaves the compiler unable to prove at the
     // loop head that V's copies do not alias the K reads, and it then waits there on
     // every tile.
     drain_then_barrier();
   }
-  for (int it = 0; it < cnt; ++it) {
-    const int key0 = list[it] * 128;
-    const bool next = it + 1 < cnt;
+  for (int it = 0; it < ntot; ++it) {
+    const int key0 = tile_key0(it);
+    const int klim = tile_limit(it);
+    const float bias = it < cnt ? 0.f : a.comp_bias;
+    const bool next = it + 1 < ntot;
     f32x16 s[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) s[t] = f32x16{};
@@ -288,15 +299,14 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
       }
     }
     drain_then_barrier();  // B1: V(it) has landed, K(it) reads are done
-    const int kb_next = next ? list[it + 1] : 0;
-    if (next) issue_k(kb_next);
+    if (next) issue_k(it + 1);
 
-    if (key0 + 128 > a.Nk) {
+    if (key0 + 128 > klim) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-          if (key0 + t * 32 + tile_key(hl, j) >= a.Nk) s[t][j] = neg_inf();
+          if (key0 + t * 32 + tile_key(hl, j) >= klim) s[t][j] = neg_inf();
     }
     float mx = neg_inf();
 #pragma unroll
@@ -304,7 +314,7 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
 #pragma unroll
       for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
     mx = fmaxf(mx, xor32(mx));
-    const float m_new = fmaxf(m_run, mx * c);
+    const float m_new = fmaxf(m_run, __builtin_fmaf(mx, c, bias));
     if (m_new != m_run) {
       const float alpha = fast_exp2(m_run - m_new);
       l_run *= alpha;
@@ -320,8 +330,8 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
       for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float v0 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e], c, -m_run));
-          const float v1 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e + 1], c, -m_run));
+          const float v0 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e], c, bias - m_run));
+          const float v1 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e + 1], c, bias - m_run));
           lsum += v0 + v1;
           p[t][u][e] = pack2<CT>(v0, v1);
         }
@@ -358,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
     }
     __builtin_amdgcn_s_setprio(0);
     drain_then_barrier();  // B2: K(it+1) has landed, V(it) reads are done
-    if (next) issue_v(kb_next);
+    if (next) issue_v(it + 1);
   }
 
   const float l = l_run + xor32(l_run);
@@ -374,7 +384,7 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
                    o[dt][4 * g + 3] * inv);
       }
     if (a.lse != nullptr && hl == 0)
-      a.lse[((int64_t)b * a.H + h) * a.Nq + qrow] = cnt > 0 ? (m_run + __log2f(l)) * kLn2 : pos_inf();
+      a.lse[((int64_t)b * a.H + h) * a.Nq + qrow] = ntot > 0 ? (m_run + __log2f(l)) * kLn2 : pos_inf();
   }
 }
 

@@ -84,13 +84,25 @@ int sinkattn_block_sparse_plan(const uint8_t* mask, const int64_t mask_strides[4
   return hip_status(sa::launch_block_sparse_plan(a, (hipStream_t)stream), "plan launch");
 }
 
-int sinkattn_block_sparse_fwd(const void* q, const void* k, const void* v, int dtype, int64_t B,
-                              int64_t H, int64_t Nq, int64_t Nk, int64_t D,
-                              const int64_t q_strides[4], const int64_t k_strides[4],
-                              const int64_t v_strides[4], void* out,
-                              const int64_t out_strides[4], float* lse, const int32_t* counts,
-                              const int32_t* idx, const int32_t* order, int64_t nqb, int64_t nkb,
-                              float softmax_scale, void* stream) {
+}  // extern "C"
+
+namespace {
+
+struct CompTiles {
+  const void* kd = nullptr;
+  const void* vd = nullptr;
+  const int64_t* kds = nullptr;
+  const int64_t* vds = nullptr;
+  int64_t Nd = 0, qblocks = 0;
+  float log_gap = 0.f;
+};
+
+int block_sparse_fwd_impl(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                          int64_t H, int64_t Nq, int64_t Nk, int64_t D, const int64_t q_strides[4],
+                          const int64_t k_strides[4], const int64_t v_strides[4], void* out,
+                          const int64_t out_strides[4], float* lse, const int32_t* counts,
+                          const int32_t* idx, const int32_t* order, int64_t nqb, int64_t nkb,
+                          float softmax_scale, const CompTiles& comp, void* stream) {
   if (!valid_dtype(dtype)) return fail("fwd: unsupported dtype %d", dtype);
   if (D != 64 && D != 128) return fail("fwd: head dim %lld not supported (64 or 128)", (long long)D);
   if (B < 0 || H < 0 || Nq < 0 || Nk < 0) return fail("fwd: negative size");
@@ -132,7 +144,145 @@ int sinkattn_block_sparse_fwd(const void* q, const void* k, const void* v, int d
   a.nqb = (int)nqb;
   a.nkb = (int)nkb;
   a.scale = softmax_scale;
+  if (comp.qblocks > 0 && comp.Nd > 0) {
+    if (dtype == SINKATTN_F32 || D != 128) return fail("fwd_comp: compensation tiles need bf16/f16 and D=128");
+    if (comp.qblocks > nqb) return fail("fwd_comp: comp_qblocks %lld exceeds %lld q-blocks", (long long)comp.qblocks, (long long)nqb);
+    if (comp.Nd > kMaxInt) return fail("fwd_comp: Nd exceeds int32");
+    if ((rc = check_operand("kd", comp.kd, comp.kds)) != 0) return rc;
+    if ((rc = check_operand("vd", comp.vd, comp.vds)) != 0) return rc;
+    if (comp.kds[2] != k_strides[2] || comp.vds[2] != v_strides[2])
+      return fail("fwd_comp: kd/vd row strides must equal k/v row strides");
+    if (!(comp.log_gap >= 0.f) || comp.log_gap > 64.f) return fail("fwd_comp: log_gap %g out of range", comp.log_gap);
+    a.kd = comp.kd;
+    a.vd = comp.vd;
+    a.kds[0] = comp.kds[0];
+    a.kds[1] = comp.kds[1];
+    a.vds[0] = comp.vds[0];
+    a.vds[1] = comp.vds[1];
+    a.Nd = (int)comp.Nd;
+    a.comp_qblocks = (int)comp.qblocks;
+    a.comp_bias = comp.log_gap * 1.4426950408889634f;
+  }
   return hip_status(sa::launch_block_sparse_fwd(a, dtype, (int)D, (hipStream_t)stream), "fwd launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int sinkattn_block_sparse_fwd(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                              int64_t H, int64_t Nq, int64_t Nk, int64_t D,
+                              const int64_t q_strides[4], const int64_t k_strides[4],
+                              const int64_t v_strides[4], void* out,
+                              const int64_t out_strides[4], float* lse, const int32_t* counts,
+                              const int32_t* idx, const int32_t* order, int64_t nqb, int64_t nkb,
+                              float softmax_scale, void* stream) {
+  return block_sparse_fwd_impl(q, k, v, dtype, B, H, Nq, Nk, D, q_strides, k_strides, v_strides, out,
+                               out_strides, lse, counts, idx, order, nqb, nkb, softmax_scale, CompTiles{},
+                               stream);
+}
+
+int sinkattn_block_sparse_fwd_comp(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                                   int64_t H, int64_t Nq, int64_t Nk, int64_t D,
+                                   const int64_t q_strides[4], const int64_t k_strides[4],
+                                   const int64_t v_strides[4], const void* kd, const void* vd,
+                                   const int64_t kd_strides[4], const int64_t vd_strides[4], int64_t Nd,
+                                   int64_t comp_qblocks, float log_gap, void* out,
+                                   const int64_t out_strides[4], float* lse, const int32_t* counts,
+                                   const int32_t* idx, const int32_t* order, int64_t nqb, int64_t nkb,
+                                   float softmax_scale, void* stream) {
+  if (comp_qblocks < 0 || Nd < 0) return fail("fwd_comp: negative size");
+  CompTiles comp;
+  comp.kd = kd;
+  comp.vd = vd;
+  comp.kds = kd_strides;
+  comp.vds = vd_strides;
+  comp.Nd = Nd;
+  comp.qblocks = comp_qblocks;
+  comp.log_gap = log_gap;
+  return block_sparse_fwd_impl(q, k, v, dtype, B, H, Nq, Nk, D, q_strides, k_strides, v_strides, out,
+                               out_strides, lse, counts, idx, order, nqb, nkb, softmax_scale, comp, stream);
+}
+
+int64_t sinkattn_mean_pool_tokens_rows(int64_t N, int64_t prefix, int64_t gap) {
+  if (N < 0 || gap < 1) return -1;
+  if (gap == 1) return N;
+  const int64_t p = prefix < 0 ? 0 : (prefix > N ? N : prefix);
+  if (p >= N) return N;
+  return p + cdiv(N - p, gap);
+}
+
+int sinkattn_mean_pool_tokens(const void* x, int dtype, int64_t B, int64_t H, int64_t N, int64_t D,
+                              const int64_t x_strides[4], int64_t prefix, int64_t gap, void* out,
+                              const int64_t out_strides[4], void* stream) {
+  if (!valid_dtype(dtype)) return fail("mean_pool_tokens: unsupported dtype %d", dtype);
+  if (B < 0 || H < 0 || N < 0 || gap < 1) return fail("mean_pool_tokens: bad size or gap");
+  const int64_t es = dtype == SINKATTN_F32 ? 4 : 2;
+  const int64_t chunks = D * es / 16;
+  if (D <= 0 || (D * es) % 16 != 0 || chunks > 256 || (chunks & (chunks - 1)) != 0)
+    return fail("mean_pool_tokens: head dim %lld unsupported (row of 16..4096 bytes, power of two)", (long long)D);
+  const int64_t nout = sinkattn_mean_pool_tokens_rows(N, prefix, gap);
+  if (B * H > 65535 || N > kMaxInt) return fail("mean_pool_tokens: sizes exceed the launch limits");
+  if (B * H * nout == 0) return 0;
+  int rc;
+  if ((rc = check_operand("x", x, x_strides)) != 0) return rc;
+  if ((rc = check_operand("out", out, out_strides)) != 0) return rc;
+  sa::TokenPoolArgs a{};
+  a.x = x;
+  a.out = out;
+  for (int i = 0; i < 4; ++i) {
+    a.xs[i] = x_strides[i];
+    a.os[i] = out_strides[i];
+  }
+  a.B = (int)B;
+  a.H = (int)H;
+  a.N = (int)N;
+  a.D = (int)D;
+  a.Nout = (int)nout;
+  a.gap = gap == 1 ? 1 : (int)gap;
+  const int64_t p = prefix < 0 ? 0 : (prefix > N ? N : prefix);
+  a.prefix = (gap == 1 || p >= N) ? (int)N : (int)p;  // identity cases copy every row
+  return hip_status(sa::launch_mean_pool_tokens(a, dtype, (hipStream_t)stream), "mean_pool_tokens launch");
+}
+
+int sinkattn_lse_mix(const void* sink_out, const int64_t sink_strides[4], const void* sink_lse,
+                     const int64_t sink_lse_strides[3], const void* dyn_out, const int64_t dyn_strides[4],
+                     const void* dyn_lse, const int64_t dyn_lse_strides[3], int dtype, int64_t B, int64_t H,
+                     int64_t N, int64_t D, float log_gap, void* out, const int64_t out_strides[4],
+                     void* stream) {
+  if (!valid_dtype(dtype)) return fail("lse_mix: unsupported dtype %d", dtype);
+  if (B < 0 || H < 0 || N < 0) return fail("lse_mix: negative size");
+  const int64_t es = dtype == SINKATTN_F32 ? 4 : 2;
+  if (D <= 0 || (D * es) % 16 != 0) return fail("lse_mix: head dim %lld unsupported (multiple of 16 bytes)", (long long)D);
+  if (B * H * N * (D * es / 16) > ((int64_t)1 << 40)) return fail("lse_mix: too large");
+  if (B * H * N == 0) return 0;
+  int rc;
+  if ((rc = check_operand("sink_out", sink_out, sink_strides)) != 0) return rc;
+  if ((rc = check_operand("dyn_out", dyn_out, dyn_strides)) != 0) return rc;
+  if ((rc = check_operand("out", out, out_strides)) != 0) return rc;
+  if (sink_lse == nullptr || dyn_lse == nullptr || sink_lse_strides == nullptr || dyn_lse_strides == nullptr)
+    return fail("lse_mix: null lse");
+  sa::MixArgs a{};
+  a.sink = sink_out;
+  a.dyn = dyn_out;
+  a.lse_s = sink_lse;
+  a.lse_d = dyn_lse;
+  a.out = out;
+  for (int i = 0; i < 4; ++i) {
+    a.ss[i] = sink_strides[i];
+    a.ds[i] = dyn_strides[i];
+    a.os[i] = out_strides[i];
+  }
+  for (int i = 0; i < 3; ++i) {
+    a.lss[i] = sink_lse_strides[i];
+    a.lds[i] = dyn_lse_strides[i];
+  }
+  a.B = (int)B;
+  a.H = (int)H;
+  a.N = (int)N;
+  a.D = (int)D;
+  a.log_gap = log_gap;
+  return hip_status(sa::launch_lse_mix(a, dtype, (hipStream_t)stream), "lse_mix launch");
 }
 
 static int fill_pool_args(sa::PoolArgs& a, const char* who, const void* q, const void* k, int dtype,

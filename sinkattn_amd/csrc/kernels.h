@@ -27,6 +27,14 @@ struct FwdArgs {
   const int32_t* order;
   int B, H, Nq, Nk, nqb, nkb;
   float scale;
+  // Compensation tiles (16-bit D=128 kernel): q-blocks below comp_qblocks also attend
+  // every key of kd/vd [B,H,Nd,D] (row strides equal to k's/v's; kds/vds = batch and head
+  // strides) with comp_bias added to the log2-domain logits.  comp_qblocks = 0: none.
+  const void* kd;
+  const void* vd;
+  int64_t kds[2], vds[2];
+  int Nd, comp_qblocks;
+  float comp_bias;
 };
 
 struct PoolArgs {
@@ -55,6 +63,28 @@ struct MaskArgs {
   uint8_t* ws_flags;  // [H*nq] workspace
 };
 
+// Token mean pooling: rows [0, prefix) copied, then groups of `gap` rows averaged
+// (a short last group repeats row N-1).  x [B,H,N,D] -> out [B,H,Nout,D].
+struct TokenPoolArgs {
+  const void* x;
+  int64_t xs[4];
+  void* out;
+  int64_t os[4];
+  int B, H, N, D, Nout, prefix, gap;
+};
+
+// out = a*sink + (1-a)*dyn with a = sigmoid(lse_s - lse_d - log_gap), per-op rounding.
+struct MixArgs {
+  const void* sink;
+  const void* dyn;
+  const void* lse_s;
+  const void* lse_d;
+  void* out;
+  int64_t ss[4], ds[4], lss[3], lds[3], os[4];
+  int B, H, N, D;
+  float log_gap;
+};
+
 constexpr int kXcds = 8;  // gfx950: work-group i is dispatched to XCD i % 8
 int plan_order_slots(int rows, int nqb);
 hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream);
@@ -64,5 +94,7 @@ int block_mass_groups();
 hipError_t launch_max_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_mean_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_coverage_mask(const MaskArgs& a, hipStream_t stream);
+hipError_t launch_mean_pool_tokens(const TokenPoolArgs& a, int dtype, hipStream_t stream);
+hipError_t launch_lse_mix(const MixArgs& a, int dtype, hipStream_t stream);
 
 }  // namespace sa

@@ -155,6 +155,133 @@ def block_sparse_attention(
     return out, lse
 
 
+def _empty_like_layout(t: torch.Tensor, rows: int) -> torch.Tensor:
+    """Uninitialised [B, H, rows, D] tensor whose dims are laid out in memory in the same
+    order as t's (so a [B, N, H, D]-memory view gets a [B, rows, H, D]-memory result and
+    the two share row-stride structure)."""
+    shape = list(t.shape)
+    shape[2] = rows
+    order = sorted(range(4), key=lambda d: (-t.stride(d), -d))  # outermost first
+    buf = torch.empty([shape[d] for d in order], dtype=t.dtype, device=t.device)
+    inv = [order.index(d) for d in range(4)]
+    return buf.permute(*inv)
+
+
+def mean_pool_tokens(x: torch.Tensor, gap: int, prefix: int = 0,
+                     like: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Rows [0, prefix) of dim 2 kept, the rest averaged in groups of `gap` (a short last
+    group repeats the last row).  x is [B, H, N, D] on the GPU.  The result has the
+    memory layout of `like` (default x) along (B, H, rows, D)."""
+    _require_cuda("mean_pool_tokens", x)
+    if x.dim() != 4:
+        raise ValueError(f"x must be [B, H, N, D], got {tuple(x.shape)}")
+    B, H, N, D = (int(s) for s in x.shape)
+    L = _lib.lib()
+    rows = int(L.sinkattn_mean_pool_tokens_rows(N, int(prefix), int(gap)))
+    if rows < 0:
+        raise ValueError(f"mean_pool_tokens: bad gap {gap}")
+    xk = _kernel_operand(x)
+    out = _empty_like_layout(like if like is not None else x, rows)
+    if not (out.stride(3) == 1 and all(s % 8 == 0 for s in out.stride()[:3])):
+        out = torch.empty((B, H, rows, D), dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.check(
+            L.sinkattn_mean_pool_tokens(
+                xk.data_ptr(), _lib.dtype_code(x.dtype), B, H, N, D, _lib.strides4(xk), int(prefix), int(gap),
+                out.data_ptr(), _lib.strides4(out), _lib.stream_ptr(x.device),
+            ),
+            "mean_pool_tokens",
+        )
+    return out
+
+
+def block_sparse_attention_comp(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    plan: BlockSparsePlan,
+    kd: torch.Tensor,
+    vd: torch.Tensor,
+    gap: int,
+    comp_rows: Optional[int] = None,
+    softmax_scale: Optional[float] = None,
+    return_lse: bool = False,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Block-sparse attention fused with the compensation branch: query rows below
+    `comp_rows` (default all; must be a multiple of 128 or Nq) also attend every key of
+    kd/vd with weight `gap` each, which equals the reference's LSE mix of the two
+    branches.  kd/vd must share k's/v's row strides (see mean_pool_tokens(like=...))."""
+    _require_cuda("block_sparse_attention_comp", q, k, v, kd, vd)
+    B, H, Nq, D = (int(x) for x in q.shape)
+    Nk, Nd = int(k.shape[2]), int(kd.shape[2])
+    if tuple(k.shape) != (B, H, Nk, D) or tuple(v.shape) != (B, H, Nk, D):
+        raise ValueError(f"k/v shapes {tuple(k.shape)}/{tuple(v.shape)} do not match q {tuple(q.shape)}")
+    if tuple(kd.shape) != (B, H, Nd, D) or tuple(vd.shape) != (B, H, Nd, D):
+        raise ValueError(f"kd/vd shapes {tuple(kd.shape)}/{tuple(vd.shape)} do not match [{B}, {H}, Nd, {D}]")
+    if not (q.dtype == k.dtype == v.dtype == kd.dtype == vd.dtype) or q.dtype == torch.float32 or D != 128:
+        raise TypeError("block_sparse_attention_comp: bf16/f16 operands of one dtype, head dim 128")
+    nqb, nkb = _cdiv(Nq, KERNEL_BLOCK), _cdiv(Nk, KERNEL_BLOCK)
+    if plan.shape != (B, H, nqb, nkb):
+        raise ValueError(f"block mask shape {plan.shape} does not match [{B}, {H}, {nqb}, {nkb}]")
+    comp_rows = Nq if comp_rows is None else int(comp_rows)
+    if comp_rows != Nq and comp_rows % KERNEL_BLOCK != 0:
+        raise ValueError(f"comp_rows {comp_rows} must be a multiple of {KERNEL_BLOCK} or Nq")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    qk, kk, vk = _kernel_operand(q), _kernel_operand(k), _kernel_operand(v)
+    kdk, vdk = _kernel_operand(kd), _kernel_operand(vd)
+    if kdk.stride(2) != kk.stride(2) or vdk.stride(2) != vk.stride(2):
+        raise ValueError("kd/vd row strides must equal k/v row strides")
+    out = torch.empty((B, Nq, H, D), dtype=q.dtype, device=q.device).permute(0, 2, 1, 3)
+    lse = torch.empty((B, H, Nq), dtype=torch.float32, device=q.device) if return_lse else None
+    L = _lib.lib()
+    with torch.cuda.device(q.device):
+        _lib.check(
+            L.sinkattn_block_sparse_fwd_comp(
+                qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), _lib.dtype_code(q.dtype), B, H, Nq, Nk, D,
+                _lib.strides4(qk), _lib.strides4(kk), _lib.strides4(vk),
+                kdk.data_ptr(), vdk.data_ptr(), _lib.strides4(kdk), _lib.strides4(vdk), Nd,
+                _cdiv(comp_rows, KERNEL_BLOCK), float(math.log(max(1, int(gap)))),
+                out.data_ptr(), _lib.strides4(out), _lib.ptr(lse),
+                plan.counts.data_ptr(), plan.idx.data_ptr(), plan.order.data_ptr(),
+                nqb, nkb, float(softmax_scale), _lib.stream_ptr(q.device),
+            ),
+            "block_sparse_fwd_comp",
+        )
+    return out, lse
+
+
+def lse_mix(sink_out: torch.Tensor, sink_lse: torch.Tensor, dyn_out: torch.Tensor, dyn_lse: torch.Tensor,
+            log_gap: float) -> torch.Tensor:
+    """out = a*sink_out + (1-a)*dyn_out, a = sigmoid(sink_lse - dyn_lse - log_gap), with
+    each step rounded to the tensors' dtype like the reference's torch ops.  Outputs
+    [B, H, N, D], LSEs [B, H, N] or [B, H, N, 1], one dtype, on the GPU."""
+    _require_cuda("lse_mix", sink_out, sink_lse, dyn_out, dyn_lse)
+    B, H, N, D = (int(x) for x in sink_out.shape)
+    if tuple(dyn_out.shape) != (B, H, N, D):
+        raise ValueError("lse_mix: output shapes differ")
+    ls = sink_lse.reshape(B, H, N) if sink_lse.dim() == 4 else sink_lse
+    ld = dyn_lse.reshape(B, H, N) if dyn_lse.dim() == 4 else dyn_lse
+    if tuple(ls.shape) != (B, H, N) or tuple(ld.shape) != (B, H, N):
+        raise ValueError("lse_mix: LSE shapes must be [B, H, N] or [B, H, N, 1]")
+    if not (sink_out.dtype == dyn_out.dtype == ls.dtype == ld.dtype):
+        raise TypeError("lse_mix: one dtype for outputs and LSEs")
+    so, do = _kernel_operand(sink_out), _kernel_operand(dyn_out)
+    out = torch.empty((B, N, H, D), dtype=sink_out.dtype, device=sink_out.device).permute(0, 2, 1, 3)
+    L = _lib.lib()
+    with torch.cuda.device(sink_out.device):
+        _lib.check(
+            L.sinkattn_lse_mix(
+                so.data_ptr(), _lib.strides4(so), ls.data_ptr(), _lib.strides3(ls),
+                do.data_ptr(), _lib.strides4(do), ld.data_ptr(), _lib.strides3(ld),
+                _lib.dtype_code(sink_out.dtype), B, H, N, D, float(log_gap),
+                out.data_ptr(), _lib.strides4(out), _lib.stream_ptr(sink_out.device),
+            ),
+            "lse_mix",
+        )
+    return out
+
+
 def block_mass_scores(q: torch.Tensor, k: torch.Tensor, block_size: int = 128,
                       scale: Optional[float] = None) -> torch.Tensor:
     """Exact per-(q-block, k-block) mean softmax mass, fp32 [B, H, nqb, nkb]."""

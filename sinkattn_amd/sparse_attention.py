@@ -102,10 +102,18 @@ def _pad_to_multiple(x: torch.Tensor, multiple: int) -> torch.Tensor:
     return F.pad(x, (0, 0, 0, multiple - rem), mode="replicate")
 
 
+def _token_pool_on_gpu(x: torch.Tensor) -> bool:
+    """GPU tensors go to the mean_pool_tokens kernel; host tensors keep the torch ops."""
+    return x.is_cuda and x.dim() == 4
+
+
 def _mean_pool_sequence(x: torch.Tensor, pool_size: int) -> torch.Tensor:
-    """Mean over groups of ``pool_size`` rows of dim 2 (sparse_attention.py:88-94)."""
+    """Mean over groups of ``pool_size`` rows of dim 2, the last group replicate-padded
+    (sparse_attention.py:88-94).  On the GPU: one mean_pool_tokens launch."""
     if pool_size <= 1:
         return x
+    if _token_pool_on_gpu(x):
+        return ops.mean_pool_tokens(x, int(pool_size), 0)
     x = _pad_to_multiple(x, pool_size)
     b, h, n, d = x.shape
     return x.view(b, h, n // pool_size, pool_size, d).mean(dim=-2)
@@ -113,15 +121,18 @@ def _mean_pool_sequence(x: torch.Tensor, pool_size: int) -> torch.Tensor:
 
 def _mean_pool_sequence_preserve_prefix(x: torch.Tensor, pool_size: int, *,
                                         prefix_tokens: int = 0) -> torch.Tensor:
-    """Keep the first ``prefix_tokens`` rows, mean-pool the rest (sparse_attention.py:97-115)."""
+    """Keep the first ``prefix_tokens`` rows, mean-pool the rest (sparse_attention.py:97-115).
+    On the GPU: one mean_pool_tokens launch (no concatenation)."""
     if pool_size <= 1:
         return x
     n = int(x.size(2))
     prefix = min(max(int(prefix_tokens), 0), n)
-    if prefix <= 0:
-        return _mean_pool_sequence(x, pool_size)
     if prefix >= n:
         return x
+    if _token_pool_on_gpu(x):
+        return ops.mean_pool_tokens(x, int(pool_size), prefix)
+    if prefix <= 0:
+        return _mean_pool_sequence(x, pool_size)
     return torch.cat([x[:, :, :prefix, :], _mean_pool_sequence(x[:, :, prefix:, :], pool_size)], dim=2)
 
 
@@ -494,6 +505,34 @@ def _block_sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_
     return out, lse.unsqueeze(-1).to(device=q.device, dtype=q.dtype)
 
 
+def _fused_compensation_supported(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    """The fused sparse + compensation kernel covers bf16/f16 GPU tensors with d = 128."""
+    return (q.is_cuda and q.dim() == 4 and q.dtype in (torch.bfloat16, torch.float16)
+            and q.dtype == k.dtype == v.dtype and int(q.size(-1)) == 128)
+
+
+def _block_sparse_attn_with_compensation(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                         block_mask: torch.Tensor, k_dynamic: torch.Tensor,
+                                         v_dynamic: torch.Tensor, sample_gap: int,
+                                         compensated_rows: Optional[int] = None) -> torch.Tensor:
+    """Sparse attention and the pooled-K/V compensation with adaptive mixing in one kernel.
+
+    The reference runs `_block_sparse_attn(..., return_lse=True)`, an attention over
+    (k_dynamic, v_dynamic) with LSE and `_mix_attention_outputs`
+    (wanx/runtime/sink_sparse_wan.py:194-265, zimg/runtime/sink_sparse_zimage.py:553-592).
+    The mix weights exp(lse_s) : gap*exp(lse_d) make the result the attention over the
+    listed keys plus every pooled key counted `sample_gap` times, which this computes in
+    one online softmax (fp32 LSEs; the reference rounds both LSEs to q.dtype first).
+    Rows at or beyond `compensated_rows` (a multiple of 128) get the sparse part only.
+    k_dynamic/v_dynamic must share k's/v's row strides (ops.mean_pool_tokens(like=k)).
+    """
+    _ensure_block_sparse_available()
+    plan = ops.PLAN_CACHE.get(block_mask if block_mask.is_cuda else block_mask.to(q.device))
+    out, _ = ops.block_sparse_attention_comp(q, k, v, plan, k_dynamic, v_dynamic, int(sample_gap),
+                                             comp_rows=compensated_rows, return_lse=False)
+    return out
+
+
 def _make_full_block_mask(batch_size: int, num_heads: int, seq_len_q: int, seq_len_k: int,
                           block_size: int, device: torch.device) -> torch.Tensor:
     return torch.ones(batch_size, num_heads, _ceil_div(seq_len_q, block_size),
@@ -563,6 +602,33 @@ def _dense_short_attention_with_lse(q: torch.Tensor, k: torch.Tensor,
     return torch.cat(outs, dim=2), torch.cat(lses, dim=2)
 
 
+_LOG_GAP_CACHE: Dict[tuple, float] = {}
+
+
+def _log_gap_value(gap, dtype: torch.dtype) -> float:
+    """The reference's ``sink_lse.new_tensor(gap).log()`` as a Python float: log of the
+    dtype-rounded gap, rounded to the dtype (evaluated once per (gap, dtype) on the host,
+    so the GPU path needs no device-to-host read)."""
+    key = (int(gap), dtype)
+    val = _LOG_GAP_CACHE.get(key)
+    if val is None:
+        val = float(torch.tensor(float(max(1, int(gap))), dtype=dtype).log().item())
+        _LOG_GAP_CACHE[key] = val
+    return val
+
+
+def _mix_on_gpu(sink_out, sink_lse, dyn_out, dyn_lse) -> bool:
+    """The lse_mix kernel covers one dtype for all four tensors, [B,H,N,D] outputs and
+    [B,H,N] / [B,H,N,1] LSEs."""
+    if not (sink_out.dim() == 4 and dyn_out.shape == sink_out.shape):
+        return False
+    if not (sink_out.dtype == dyn_out.dtype == sink_lse.dtype == dyn_lse.dtype):
+        return False
+    want = tuple(sink_out.shape[:3])
+    return all(t.is_cuda and tuple(t.shape[:3]) == want and (t.dim() == 3 or (t.dim() == 4 and t.shape[3] == 1))
+               for t in (sink_lse, dyn_lse)) and dyn_out.is_cuda
+
+
 def _mix_attention_outputs(sink_out: torch.Tensor, sink_lse: Optional[torch.Tensor],
                            dynamic_out: torch.Tensor, dynamic_lse: Optional[torch.Tensor],
                            config: SinkSparseConfig, dynamic_sample_gap: Optional[int] = None) -> torch.Tensor:
@@ -573,6 +639,8 @@ def _mix_attention_outputs(sink_out: torch.Tensor, sink_lse: Optional[torch.Tens
     if sink_lse is None or dynamic_lse is None:
         raise ValueError("Adaptive Sink-Sparse mixing requires both sink_lse and dynamic_lse.")
     gap = config.sample_gap if dynamic_sample_gap is None else int(dynamic_sample_gap)
+    if sink_out.is_cuda and _mix_on_gpu(sink_out, sink_lse, dynamic_out, dynamic_lse):
+        return ops.lse_mix(sink_out, sink_lse, dynamic_out, dynamic_lse, _log_gap_value(gap, sink_lse.dtype))
     log_gap = sink_lse.new_tensor(float(max(1, int(gap)))).log()
     w_s = sink_lse
     w_d = dynamic_lse + log_gap

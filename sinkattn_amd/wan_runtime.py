@@ -20,6 +20,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import ops
 from .sparse_attention import (
     SinkMaskCalibrator,
     SinkRuntimeState,
@@ -27,11 +28,13 @@ from .sparse_attention import (
     _BLOCK_SPARSE_KERNEL_BLOCK_SIZE,
     _adapt_block_mask_for_kernel,
     _block_sparse_attn,
+    _block_sparse_attn_with_compensation,
     _build_offline_required_mask,
     _ceil_div,
     _dense_short_attention,
     _dense_short_attention_with_lse,
     _device_cache_key,
+    _fused_compensation_supported,
     _make_full_block_mask,
     _mean_pool_sequence_preserve_prefix,
     _mix_attention_outputs,
@@ -47,6 +50,12 @@ __all__ = [
     "set_sink_calibration_attn_wanx",
     "set_sink_sparse_attn_wanx",
 ]
+
+
+# With adaptive mixing the sparse call, the pooled-K/V attention and the LSE mix run as
+# one kernel (sparse tiles then the pooled tiles, with ln(sample_gap) added to the pooled
+# logits).  False runs the reference's three separate steps on the GPU kernels instead.
+FUSE_COMPENSATION = True
 
 
 def _section(runtime_state: Optional[SinkRuntimeState], name: str):
@@ -169,6 +178,15 @@ class WanSinkSparseInnerAttention(nn.Module):
             if mode == "none":
                 with _section(rs, "sparse_main"):
                     out, _ = _block_sparse_attn(q, k, v, mask, return_lse=False)
+            elif (self.config.mixing_mode == "adaptive" and FUSE_COMPENSATION
+                  and _fused_compensation_supported(q, k, v)):
+                with _section(rs, "comp_pool"):
+                    prefix = max(int(self.config.text_length), 0)
+                    k_dyn = ops.mean_pool_tokens(k, gap, prefix, like=k)
+                    v_dyn = ops.mean_pool_tokens(v, gap, prefix, like=v)
+                    dyn_len = int(k_dyn.size(2))
+                with _section(rs, "sparse_main"):  # sparse + compensation + mix
+                    out = _block_sparse_attn_with_compensation(q, k, v, mask, k_dyn, v_dyn, gap)
             else:
                 adaptive = self.config.mixing_mode == "adaptive"
                 with _section(rs, "sparse_main"):

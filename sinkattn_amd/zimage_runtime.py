@@ -21,15 +21,18 @@ from typing import Any, Dict, Optional
 import torch
 import torch.nn.functional as F
 
+from . import ops
 from .sparse_attention import (
     SinkRuntimeState,
     SinkSparseConfig,
     _block_sparse_attn,
+    _block_sparse_attn_with_compensation,
     _build_direct_mean_coverage_mask,
     _ceil_div,
     _compute_block_scores,
     _dense_short_attention_with_lse,
     _device_cache_key,
+    _fused_compensation_supported,
     _mean_pool_sequence,
     _mix_attention_outputs,
     load_sink_mask_package,
@@ -37,6 +40,11 @@ from .sparse_attention import (
 
 SEQ_MULTI_OF = 32
 DEFAULT_TEXT_LENGTH = 512
+
+# Image rows run sparse attention, the pooled-K/V attention and the LSE mix as one kernel
+# when the image prefix is a whole number of 128-token blocks; False keeps the
+# reference's three separate steps (on the GPU kernels).
+FUSE_COMPENSATION = True
 
 __all__ = [
     "DEFAULT_TEXT_LENGTH",
@@ -425,6 +433,20 @@ class ZImageStaticSinkProcessor:
                         out_i = _dense_attention(q_i, k_i, v_i)
                     mask = torch.ones_like(mask, dtype=torch.bool)
                     run_mode = "forced_dense_step" if dense_step else "forced_dense_layer"
+                elif (mode == "pooled_kv" and FUSE_COMPENSATION and self.image_token_count % 128 == 0
+                      and _fused_compensation_supported(q_i, k_i, v_i)):
+                    il = self.image_token_count
+                    with sec("comp_pool"):
+                        dyn_k = ops.mean_pool_tokens(k_i[:, :, :il], gap)
+                        dyn_v = ops.mean_pool_tokens(v_i[:, :, :il], gap)
+                        if text_tokens > 0:
+                            dyn_k = torch.cat([dyn_k, k_i[:, :, il:n]], dim=2)
+                            dyn_v = torch.cat([dyn_v, v_i[:, :, il:n]], dim=2)
+                        dyn_len = int(dyn_k.size(2))
+                    with sec("sparse_main"):  # sparse + compensation on the image rows + mix
+                        out_i = _block_sparse_attn_with_compensation(q_i, k_i, v_i, mask, dyn_k, dyn_v, gap,
+                                                                     compensated_rows=il)
+                    run_mode = mode
                 else:
                     with sec("sparse_main"):
                         out_i, sink_lse = _block_sparse_attn(q_i, k_i, v_i, mask, return_lse=mode == "pooled_kv")
