@@ -260,6 +260,35 @@ def main():
                           "mfma_frac": round(pool_flops / (pms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
                           "traffic": traffic_bytes("pool"),
                           "kernel": "sa::block_mass_persistent_kernel<0> (bf16)"}
+        # the full Wan layer call with the default compensation branch (pooled_kv, gap 30,
+        # adaptive mix): fused kernel vs the reference's three steps on this build's kernels
+        from sinkattn_amd import sparse_attention as sa
+        gap = 30
+        cfg = sa.SinkSparseConfig(sample_gap=gap)
+
+        def fused():
+            kd = ops.mean_pool_tokens(k, gap, 0, like=k)
+            vd = ops.mean_pool_tokens(v, gap, 0, like=v)
+            return ops.block_sparse_attention_comp(q, k, v, plan, kd, vd, gap)
+
+        fplan_d = ops.block_sparse_plan(torch.ones(B, H, 256, 9, dtype=torch.bool, device=dev))
+
+        def unfused():
+            so, sl = ops.block_sparse_attention(q, k, v, plan, return_lse=True)
+            kd = ops.mean_pool_tokens(k, gap, 0, like=k)
+            vd = ops.mean_pool_tokens(v, gap, 0, like=v)
+            do, dl = ops.block_sparse_attention(q, kd, vd, fplan_d, return_lse=True)
+            return sa._mix_attention_outputs(so, sl.unsqueeze(-1).to(q.dtype), do, dl.unsqueeze(-1).to(q.dtype), cfg)
+
+        fms = time_fn(torch, fused, max(3, args.steps // 2), 1)
+        ums = time_fn(torch, unfused, max(3, args.steps // 2), 1)
+        pus = time_fn(torch, lambda: ops.mean_pool_tokens(k, gap, 0, like=k), 10, 2) * 1e3
+        pool_rd = k.numel() * 2 + (N + gap - 1) // gap * B * H * D * 2
+        out["wan_layer_with_compensation"] = {
+            "fused_ms": round(fms, 4), "unfused_ms": round(ums, 4),
+            "mean_pool_tokens_us": round(pus, 1),
+            "mean_pool_tokens_hbm_gbs": round(pool_rd / (pus * 1e-6) / 1e9, 1),
+            "note": "sparse attention + K/V mean-pool by 30 + attention over the 1092 pooled keys + LSE mix"}
         scores = torch.rand(H, 256, 256, device=dev)
         scores = scores / scores.sum(-1, keepdim=True)
         mus = time_fn(torch, lambda: ops.coverage_mask(scores, 0.85, True), 10, 2) * 1e3
