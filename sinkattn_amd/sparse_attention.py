@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import math
 import os
+import weakref
 from dataclasses import asdict, dataclass
 from pathlib import Path
 from typing import Dict, Iterable, Optional, Tuple
@@ -275,14 +276,30 @@ class SinkRuntimeState:
             return 0.0
         return float(sum(float(e[key]) for e in events) / len(events))
 
+    def _cached_density(self, mask: Optional[torch.Tensor]) -> float:
+        """Density of a mask, computed once per mask object (and content version).  The
+        runtimes pass the same cached kernel mask on every call, so the device-to-host
+        read happens on the first call only, not on every layer call as in the reference."""
+        if mask is None:
+            return 0.0
+        key = id(mask)
+        sig = (mask._version, mask.data_ptr(), tuple(mask.shape), str(mask.device))
+        ent = self._density_cache.get(key)
+        if ent is not None and ent[0]() is mask and ent[1] == sig:
+            return ent[2]
+        val = self._mask_density(mask)
+        cache = self._density_cache
+        cache[key] = (weakref.ref(mask, lambda _r, k=key: cache.pop(k, None)), sig, val)
+        return val
+
     def record_mask_stats(self, *, layer_idx: int, sink_mask_tag: str, dynamic_mode: str,
                           dynamic_sample_gap: int, base_runtime_mask: torch.Tensor,
                           topup_mask: Optional[torch.Tensor] = None,
                           dynamic_seq_len_k: Optional[int] = None,
                           total_seq_len_k: Optional[int] = None) -> None:
-        base = self._mask_density(base_runtime_mask)
-        topup = self._mask_density(topup_mask)
-        combined = self._mask_density(base_runtime_mask if topup_mask is None else (base_runtime_mask | topup_mask))
+        base = self._cached_density(base_runtime_mask)
+        topup = self._cached_density(topup_mask)
+        combined = base if topup_mask is None else self._mask_density(base_runtime_mask | topup_mask)
         ratio = 0.0
         if dynamic_seq_len_k is not None and total_seq_len_k is not None and total_seq_len_k > 0:
             ratio = float(dynamic_seq_len_k) / float(total_seq_len_k)
@@ -343,7 +360,14 @@ class SinkRuntimeState:
 # --- calibration (a5) ------------------------------------------------------------------------
 class SinkMaskCalibrator:
     """Accumulates per-layer block scores over calibration calls and builds the mask
-    package (sparse_attention.py:526-608)."""
+    package (sparse_attention.py:526-608).
+
+    The reference copies every call's batch-mean map to the host (a device sync per layer
+    call) and accumulates there.  Here the per-layer fp32 sums stay on the device the
+    scores were computed on; the accumulation is elementwise fp32 adds and squares (exact
+    IEEE operations on either side), and `build_package` copies the sums to the host once
+    and finishes there like the reference, so the package is bit-identical to host
+    accumulation."""
 
     def __init__(self, config: SinkSparseConfig):
         self.config = config
@@ -371,21 +395,25 @@ class SinkMaskCalibrator:
         for layer_idx in sorted(self.score_sums):
             key = str(layer_idx)
             n = self.score_counts[layer_idx]
-            mean = self.score_sums[layer_idx] / n
-            second = self.score_sq_sums[layer_idx] / n
+            # the divisions on the host, as the reference does them (a GPU tensor / scalar
+            # division is a multiply by the reciprocal, which can differ in the last bit)
+            mean = self.score_sums[layer_idx].cpu() / n
+            second = self.score_sq_sums[layer_idx].cpu() / n
             std = torch.sqrt((second - mean.square()).clamp_min_(0.0))
             mean_scores[key] = mean
             std_scores[key] = std
-            sink_masks[key] = _build_direct_mean_coverage_mask(mean, config)
+            sink_masks[key] = _build_direct_mean_coverage_mask(mean, config).cpu()
             counts[key] = int(n)
         return mean_scores, std_scores, sink_masks, counts
 
     @torch.no_grad()
     def record(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Block scores of one call on the GPU kernels; their batch mean is added to the
+        layer's device-resident sums (no host copy, no sync)."""
         if layer_idx == 0:
             self.current_step += 1
         samples = _compute_block_scores(q, k, v, self.config).detach().float()
-        self._accumulate_score(layer_idx, samples.mean(dim=0).cpu())
+        self._accumulate_score(layer_idx, samples.mean(dim=0))
 
     def build_package(self, include_scores: bool = True,
                       config_override: Optional[SinkSparseConfig] = None) -> dict:

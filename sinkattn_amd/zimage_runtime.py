@@ -231,7 +231,8 @@ def prepare_zimage_attention_tensors(attn: Any, hidden_states: torch.Tensor, *,
 class ZImageSinkMaskCalibrator:
     """Per-layer sums of aligned scores, of their squares and of the presence mask; the
     package's mean/std divide by presence (clamped to 1), so cells a call never covered
-    do not dilute the mean (sink_sparse_zimage.py:248-366)."""
+    do not dilute the mean (sink_sparse_zimage.py:248-366).  The sums live on the device
+    the scores come from (no per-call host copy); the package holds host tensors."""
 
     def __init__(self, config: SinkSparseConfig):
         self.config = build_zimg_sink_config(package_config=asdict(config))
@@ -273,7 +274,9 @@ class ZImageSinkMaskCalibrator:
         samples = _compute_block_scores(q, k, v, self.config).detach().float()
         if samples.size(0) != 1:
             raise ValueError("Z-Image calibration expects one sample at a time after valid-token slicing.")
-        scores = samples.mean(dim=0).cpu()
+        # stays on the scores' device: alignment and accumulation are copies and
+        # elementwise fp32 adds, identical to the reference's host accumulation
+        scores = samples.mean(dim=0)
         text_blocks = _ceil_div(int(text_token_count), int(self.config.block_size))
         aligned = _align_scores_image_text_suffix(scores, image_blocks=self.image_blocks,
                                                   current_text_blocks=text_blocks, total_blocks=self.total_blocks)
@@ -287,12 +290,13 @@ class ZImageSinkMaskCalibrator:
         means, stds, masks, counts = {}, {}, {}, {}
         for layer in sorted(self.score_sums):
             key = str(layer)
-            presence = self.score_presence_sums[layer].clamp_min_(1.0)
-            mean = self.score_sums[layer] / presence
-            var = (self.score_sq_sums[layer] / presence - mean.square()).clamp_min_(0.0)
+            # finished on the host like the reference (one copy of the sums per layer)
+            presence = self.score_presence_sums[layer].cpu().clamp_min_(1.0)
+            mean = self.score_sums[layer].cpu() / presence
+            var = (self.score_sq_sums[layer].cpu() / presence - mean.square()).clamp_min_(0.0)
+            masks[key] = _build_direct_mean_coverage_mask(mean, cfg).cpu()
             means[key] = mean
             stds[key] = torch.sqrt(var)
-            masks[key] = _build_direct_mean_coverage_mask(mean, cfg)
             counts[key] = int(self.score_counts[layer])
         return {
             "version": 3,

@@ -213,3 +213,20 @@ def test_calibrator_accumulation_math(monkeypatch):
     assert cal.current_step == 2  # every layer-0 record starts a step
     pkg2 = cal.build_package(include_scores=False)
     assert pkg2["mean_scores"] == {} and "0" in pkg2["sink_masks"]
+
+
+def test_runtime_stats_density_is_cached_per_mask():
+    st = sa.SinkRuntimeState()
+    m = torch.zeros(1, 2, 4, 4, dtype=torch.bool)
+    m[..., 0] = True
+    calls = []
+    real = sa.SinkRuntimeState._mask_density
+    st._mask_density = lambda mask: calls.append(1) or real(mask)
+    for _ in range(3):
+        st.record_mask_stats(layer_idx=0, sink_mask_tag="t", dynamic_mode="none", dynamic_sample_gap=1,
+                             base_runtime_mask=m)
+    assert len(calls) == 1 and st.sparsity_events[-1]["base_density"] == 0.25
+    m[..., 1] = True  # in-place change bumps the version: recomputed
+    st.record_mask_stats(layer_idx=0, sink_mask_tag="t", dynamic_mode="none", dynamic_sample_gap=1,
+                         base_runtime_mask=m)
+    assert len(calls) == 2 and st.sparsity_events[-1]["combined_density"] == 0.5

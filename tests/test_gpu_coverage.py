@@ -125,3 +125,26 @@ def test_calibrator_end_to_end_matches_reference_math():
         assert mean.device.type == "cpu"
         assert torch.equal(pkg["sink_masks"][key], torch_ref.coverage_mask(mean))
         assert pkg["counts"][key] == 2
+
+
+def test_calibrator_device_accumulation_is_bit_identical():
+    """Sums stay on the GPU (no per-call host copy) and give the same bits as the
+    reference's host accumulation of the same per-call batch means."""
+    torch.manual_seed(1)
+    cfg = sa.SinkSparseConfig(pooling_mode="exact")
+    cal = sa.SinkMaskCalibrator(cfg)
+    host_sum, host_sq = None, None
+    for step in range(3):
+        q = torch.randn(2, 2, 700, 128, device="cuda", dtype=torch.bfloat16)
+        k = torch.randn(2, 2, 700, 128, device="cuda", dtype=torch.bfloat16)
+        cal.record(0, q, k, k)
+        m = sa._compute_block_scores(q, k, k, cfg).float().mean(dim=0).cpu()
+        host_sum = m.clone() if host_sum is None else host_sum + m
+        host_sq = m.square() if host_sq is None else host_sq + m.square()
+    assert cal.score_sums[0].is_cuda
+    pkg = cal.build_package()
+    mean = host_sum / 3
+    std = torch.sqrt((host_sq / 3 - mean.square()).clamp_min_(0.0))
+    assert torch.equal(pkg["mean_scores"]["0"], mean)
+    assert torch.equal(pkg["std_scores"]["0"], std)
+    assert torch.equal(pkg["sink_masks"]["0"], torch_ref.coverage_mask(mean))
