@@ -322,50 +322,61 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
       for (int i = 0; i < DT; ++i) o[i] *= alpha;
       m_run = m_new;
     }
+    // P in the MFMA's 16-bit type; the row sum adds those rounded values (one dot2 per
+    // pair, four independent partial sums), so O and l are normalised by the same weights.
     u32x4 p[4][2];
-    float lsum = 0.f;
+    float lsum[4] = {0.f, 0.f, 0.f, 0.f};
+    auto make_p = [&](int t, int u) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float v0 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e], c, bias - m_run));
-          const float v1 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e + 1], c, bias - m_run));
-          lsum += v0 + v1;
-          p[t][u][e] = pack2<CT>(v0, v1);
-        }
-    l_run += lsum;
+      for (int e = 0; e < 4; ++e) {
+        const float v0 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e], c, bias - m_run));
+        const float v1 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e + 1], c, bias - m_run));
+        p[t][u][e] = pack2<CT>(v0, v1);
+        lsum[t] = sum2_acc<CT>(p[t][u][e], lsum[t]);
+      }
+    };
+    // V^T operand for d-tile dt of step (t, u): two transpose reads.
+    auto vread = [&](int dt, int t, int u) -> u32x4 {
+      const uint32_t off = t * 8192 + u * 4096;
+      const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][0] + off));
+      const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][1] + off));
+      const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
+      return u32x4{y0[0], y0[1], y1[0], y1[1]};
+    };
+    make_p(0, 0);
 
-    // Raised issue priority over the PV MFMAs: the other wave on this SIMD (another
-    // work-group) then fills the VALU slots with its softmax instead of competing
-    // with these MFMAs for issue.
+    // PV over 8 steps (t, u) of 16 keys.  Pinned order: under each of a step's 4 MFMAs, the
+    // 2 transpose reads and about a quarter of the exp/convert/sum work of the next step,
+    // so the matrix core, the LDS pipe and the VALU all stay busy.  Raised issue priority
+    // over this loop: the other wave on the SIMD (another work-group) fills the leftover
+    // VALU slots with its own softmax instead of competing for MFMA issue.
     __builtin_amdgcn_s_setprio(1);
     {
-      // V^T operands one (t, u) step ahead: 4 d-tiles per step.
-      auto vread = [&](int dt, int t, int u) -> u32x4 {
-        const uint32_t off = t * 8192 + u * 4096;
-        const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][0] + off));
-        const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][1] + off));
-        const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
-        return u32x4{y0[0], y0[1], y1[0], y1[1]};
-      };
-      u32x4 cur[DT], nxt[DT];
+      u32x4 vr[2][DT];
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) cur[dt] = vread(dt, 0, 0);
+      for (int dt = 0; dt < DT; ++dt) vr[0][dt] = vread(dt, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
       for (int step = 0; step < 8; ++step) {
         const int t = step >> 1, u = step & 1;
+        const int nt = (step + 1) >> 1, nu = (step + 1) & 1;
         if (step + 1 < 8) {
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) nxt[dt] = vread(dt, (step + 1) >> 1, (step + 1) & 1);
+          for (int dt = 0; dt < DT; ++dt) vr[(step + 1) & 1][dt] = vread(dt, nt, nu);
+          make_p(nt, nu);
         }
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[dt] = mfma32x32x16<CT>(cur[dt], p[t][u], o[dt]);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) cur[dt] = nxt[dt];
+        for (int dt = 0; dt < DT; ++dt) {
+          o[dt] = mfma32x32x16<CT>(vr[step & 1][dt], p[t][u], o[dt]);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (step + 1 < 8) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+          }
+        }
       }
     }
+    l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
     __builtin_amdgcn_s_setprio(0);
     drain_then_barrier();  // B2: K(it+1) has landed, V(it) reads are done
     if (next) issue_v(it + 1);
@@ -591,17 +602,85 @@ __global__ __launch_bounds__(256) void plan_rows_kernel(PlanArgs a) {
   if (lane == 0) a.counts[row] = base;
 }
 
-// Launch order.  Work-group i runs on XCD i % 8 and each XCD has its own L2, so the
-// order gives XCD x the q-blocks qb = x (mod 8) of every (b, h), head by head: the
-// work-groups resident on one XCD at a time share one or two heads' K/V, which they
-// walk in the same ascending key-block order, and every XCD gets the same share of
-// every head (balanced whatever the per-head densities).  Within one (b, h, x) slice
-// the q-blocks run longest-first.  Slots past the end of a shorter slice hold -1.
+// Launch order.  Work-group i of the forward runs on XCD i % 8, so the order array decides
+// which q-blocks share an XCD's L2 (4 MB).  The q-blocks of one head read the same K/V,
+// so the resident work-groups of an XCD (32 CUs x 2) should come from one head at a
+// time.  Each head is cut into chunks of about kChunkQb q-blocks (qb = j mod C, C =
+// chunks per head); chunks are dealt to the 8 XCDs longest-processing-time first (cost
+// = listed tiles + one per q-block), at most ceil(chunks / 8) per XCD, so every XCD
+// gets the same number of chunks and nearly the same work whatever the per-head
+// densities; an XCD runs its chunks in (head, j) order and a chunk's q-blocks longest
+// first.  Slots past the end of a shorter chunk hold -1.
+constexpr int kChunkQb = 128;
+constexpr int kMaxChunks = 4096;
+
+__host__ __device__ inline int chunks_per_head(int nqb) {
+  const int c = nqb / kChunkQb;
+  return c < 1 ? 1 : c;
+}
+
 __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
-  const int slices = (a.nqb + kXcds - 1) / kXcds;  // slots per (b, h) per XCD
+  __shared__ int cost[kMaxChunks];
+  __shared__ int16_t sorted[kMaxChunks];
+  __shared__ uint8_t xcd[kMaxChunks];
+  __shared__ int16_t pos[kMaxChunks];
+  const int nbh = a.rows / a.nqb;
+  const int C = chunks_per_head(a.nqb);
+  const int S = (a.nqb + C - 1) / C;  // q-blocks per chunk (at most)
+  const int nch = nbh * C;
+  const int per_xcd = (nch + kXcds - 1) / kXcds;
+  const int total = per_xcd * S * kXcds;
+  for (int i = threadIdx.x; i < total; i += blockDim.x) a.order[i] = -1;
+  for (int ch = threadIdx.x; ch < nch; ch += blockDim.x) {
+    const int bh = ch / C, j = ch - bh * C;
+    int w = 0;
+    for (int qb = j; qb < a.nqb; qb += C) w += a.counts[bh * a.nqb + qb] + 1;
+    cost[ch] = w;
+  }
+  __syncthreads();
+  for (int ch = threadIdx.x; ch < nch; ch += blockDim.x) {  // rank by cost desc, index asc
+    const int w = cost[ch];
+    int r = 0;
+    for (int c2 = 0; c2 < nch; ++c2) r += (cost[c2] > w) || (cost[c2] == w && c2 < ch);
+    sorted[r] = (int16_t)ch;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int load[kXcds], n[kXcds];
+    for (int x = 0; x < kXcds; ++x) load[x] = n[x] = 0;
+    for (int r = 0; r < nch; ++r) {
+      const int ch = sorted[r];
+      int best = -1;
+      for (int x = 0; x < kXcds; ++x)
+        if (n[x] < per_xcd && (best < 0 || load[x] < load[best])) best = x;
+      xcd[ch] = (uint8_t)best;
+      load[best] += cost[ch];
+      ++n[best];
+    }
+    for (int x = 0; x < kXcds; ++x) n[x] = 0;
+    for (int ch = 0; ch < nch; ++ch) pos[ch] = (int16_t)(n[xcd[ch]]++);
+  }
+  __syncthreads();
+  for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
+    const int bh = row / a.nqb, qb = row - bh * a.nqb;
+    const int j = qb % C, ch = bh * C + j;
+    const int c = a.counts[row];
+    int rank = 0;
+    for (int q2 = j; q2 < a.nqb; q2 += C) {
+      const int c2 = a.counts[bh * a.nqb + q2];
+      rank += (c2 > c) || (c2 == c && q2 < qb);
+    }
+    a.order[(pos[ch] * S + rank) * kXcds + xcd[ch]] = row;
+  }
+}
+
+// Fallback when a plan has more chunks than the ordering kernel holds: XCD x gets the
+// q-blocks qb = x (mod 8) of every head, head by head, longest first within a head.
+__global__ __launch_bounds__(256) void plan_order_interleaved_kernel(PlanArgs a) {
+  const int slices = (a.nqb + kXcds - 1) / kXcds;
   const int total = a.rows / a.nqb * slices * kXcds;
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) a.order[i] = -1;
-  __syncthreads();  // launched as a single work-group: the fill precedes every placement
+  for (int i = threadIdx.x; i < total; i += blockDim.x) a.order[i] = -1;
+  __syncthreads();
   for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
     const int bh = row / a.nqb, qb = row - bh * a.nqb;
     const int x = qb % kXcds;
@@ -615,9 +694,14 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
   }
 }
 
+static bool chunked_order(int rows, int nqb) { return rows / nqb * chunks_per_head(nqb) <= kMaxChunks; }
+
 int plan_order_slots(int rows, int nqb) {
   if (rows == 0 || nqb == 0) return 0;
-  return rows / nqb * ((nqb + kXcds - 1) / kXcds) * kXcds;
+  const int nbh = rows / nqb;
+  if (!chunked_order(rows, nqb)) return nbh * ((nqb + kXcds - 1) / kXcds) * kXcds;
+  const int C = chunks_per_head(nqb);
+  return (nbh * C + kXcds - 1) / kXcds * ((nqb + C - 1) / C) * kXcds;
 }
 
 hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream) {
@@ -625,7 +709,10 @@ hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream) {
   plan_rows_kernel<<<(a.rows + 3) / 4, 256, 0, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.order == nullptr) return e;
-  plan_order_kernel<<<1, 256, 0, stream>>>(a);
+  if (chunked_order(a.rows, a.nqb))
+    plan_order_kernel<<<1, 256, 0, stream>>>(a);
+  else
+    plan_order_interleaved_kernel<<<1, 256, 0, stream>>>(a);
   return hipGetLastError();
 }
 

@@ -125,29 +125,62 @@ def test_head_dim_64_and_cross_lengths():
     _check(out, lse[..., 0], q, k, v, mask)
 
 
-def test_plan_lists_and_order():
-    mask = _random_mask(2, 3, 7, 9, 0.35, seed=12, diag=False, col0=False, empty_rows=1)
+def _check_order(plan, counts, nbh, nqb):
+    """Launch-order invariants: a permutation of the rows; slot i runs on XCD i % 8;
+    a head is cut into C = max(1, nqb // 128) chunks (qb mod C), each chunk on one XCD,
+    at most ceil(chunks / 8) chunks per XCD, run in (head, chunk) order, each chunk's
+    q-blocks longest first; LPT keeps the XCD loads within one chunk's cost."""
+    order = plan.order.cpu().tolist()
+    rows = nbh * nqb
+    real = sorted(r for r in order if r >= 0)
+    assert real == list(range(rows))
+    C = max(1, nqb // 128)
+    S = -(-nqb // C)
+    nch = nbh * C
+    per_xcd = -(-nch // 8)
+    assert len(order) == per_xcd * S * 8
+    chunk_xcd, seq = {}, {x: [] for x in range(8)}
+    for i, r in enumerate(order):
+        if r < 0:
+            continue
+        bh, qb = divmod(r, nqb)
+        ch = bh * C + qb % C
+        assert chunk_xcd.setdefault(ch, i % 8) == i % 8
+        seq[i % 8].append((i // 8, ch, int(counts[r])))
+    load = [0] * 8
+    for x in range(8):
+        chs = []
+        for k, ch, c in seq[x]:
+            if not chs or chs[-1] != ch:
+                chs.append(ch)
+            load[x] += c + 1
+        assert chs == sorted(chs) and len(chs) <= per_xcd
+        for ch in chs:  # a chunk's q-blocks in slots pos*S .. pos*S + S-1, longest first
+            ks = [k for k, c2, _ in seq[x] if c2 == ch]
+            cs = [c for _, c2, c in seq[x] if c2 == ch]
+            pos = chs.index(ch)
+            assert all(pos * S <= k < (pos + 1) * S for k in ks)
+            assert cs == sorted(cs, reverse=True)
+    chunk_cost = [0] * nch
+    for r in range(rows):
+        bh, qb = divmod(r, nqb)
+        chunk_cost[bh * C + qb % C] += int(counts[r]) + 1
+    busy = [l for l in load if l > 0]
+    assert max(busy) - min(load if nch >= 8 else busy) <= max(chunk_cost)
+
+
+@pytest.mark.parametrize("B,H,nqb,nkb,density", [(2, 3, 7, 9, 0.35), (1, 5, 300, 40, 0.3), (2, 12, 256, 256, 0.2)])
+def test_plan_lists_and_order(B, H, nqb, nkb, density):
+    mask = _random_mask(B, H, nqb, nkb, density, seed=12, diag=False, col0=False, empty_rows=1)
     plan = ops.block_sparse_plan(mask)
     counts = plan.counts.cpu()
-    idx = plan.idx.cpu().view(-1, 9)
-    flat = mask.cpu().view(-1, 9)
+    idx = plan.idx.cpu().view(-1, nkb)
+    flat = mask.cpu().view(-1, nkb)
     for r in range(flat.shape[0]):
         want = torch.nonzero(flat[r]).flatten().to(torch.int32)
         assert counts[r].item() == want.numel()
         assert torch.equal(idx[r, : want.numel()], want)
-    order = plan.order.cpu()
-    real = order[order >= 0]
-    assert torch.equal(real.sort().values, torch.arange(flat.shape[0], dtype=torch.int32))
-    # slot i runs on XCD i % 8: XCD x holds the q-blocks qb = x mod 8, longest first per head
-    nqb = 7
-    for i, row in enumerate(order.tolist()):
-        if row >= 0:
-            assert (row % nqb) % 8 == i % 8
-    for bh in range(6):
-        for x in range(8):
-            slot_rows = [r for i, r in enumerate(order.tolist()) if r >= 0 and r // nqb == bh and i % 8 == x]
-            cs = [int(counts[r]) for r in slot_rows]
-            assert cs == sorted(cs, reverse=True)
+    _check_order(plan, counts, B * H, nqb)
 
 
 def test_bad_mask_shape_raises():

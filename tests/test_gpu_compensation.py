@@ -152,7 +152,10 @@ def test_fused_compensation_vs_oracle(N, gap, prefix, comp_rows, seed):
     err = (out.float().cpu() - want).abs()
     print(f"  vs fp32 union: max {err.max().item():.3e} mean {err.mean().item():.3e}", flush=True)
     assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
-    assert (lse.cpu() - want_lse).abs().max().item() <= 1e-3
+    # the kernel's row sums add the bf16-rounded P values it multiplies V with (relative
+    # error <= 2^-9 per value), so the LSE is within 2^-8 of the fp32 one
+    lerr = (lse.cpu() - want_lse).abs()
+    assert lerr.max().item() <= 2.0 ** -8 and lerr.mean().item() <= 5e-4
     # against the reference's unfused sequence (bf16 LSEs into the reference-rounded mix)
     so, sl = sa._block_sparse_attn(q, k, v, m.to(DEV), return_lse=True)
     full = torch.ones(B, H, -(-cr // 128), -(-kd.size(2) // 128), dtype=torch.bool, device=DEV)
@@ -172,7 +175,7 @@ def test_fused_compensation_vs_oracle(N, gap, prefix, comp_rows, seed):
     so_c, do_c = so[:, :, :cr].float(), do.float()
     shift = ((sl[:, :, :cr].float().abs() + dl.float().abs() + math.log(gap)) / 4 + 4) * u
     bound = torch.full_like(err2, 2e-2)
-    bound[:, :, :cr] += shift * (so_c - do_c).abs() + 2 * u * (so_c.abs() + do_c.abs())
+    bound[:, :, :cr] += shift * (so_c - do_c).abs() + 8 * u * (so_c.abs() + do_c.abs())
     assert bool((err2 <= bound).all()), f"max excess {(err2 - bound).max().item():.3e}"
     if cr < N:  # rows past comp_rows are the plain sparse result
         assert torch.equal(out[:, :, cr:], so[:, :, cr:])
