@@ -284,6 +284,30 @@ def main():
         ums = time_fn(torch, unfused, max(3, args.steps // 2), 1)
         pus = time_fn(torch, lambda: ops.mean_pool_tokens(k, gap, 0, like=k), 10, 2) * 1e3
         pool_rd = k.numel() * 2 + (N + gap - 1) // gap * B * H * D * 2
+        # QK-norm + rotary in front of the attention: the fused kernel vs torch ops
+        C = H * D
+        xq = torch.randn(B, N, C, device=dev, dtype=torch.bfloat16)
+        xk = torch.randn(B, N, C, device=dev, dtype=torch.bfloat16)
+        wq = torch.rand(C, device=dev) + 0.5
+        wk = torch.rand(C, device=dev) + 0.5
+        ang = torch.randn(N, D // 2, device=dev)
+        fre, fim = torch.cos(ang), torch.sin(ang)
+        nq = torch.nn.RMSNorm(C, eps=1e-6).to(dev, torch.bfloat16)
+
+        def qk_torch():
+            from sinkattn_amd.wan_runtime import apply_rotary_qk
+            a, b = nq(xq), nq(xk)
+            a = a.unflatten(2, (H, D)).transpose(1, 2)
+            b = b.unflatten(2, (H, D)).transpose(1, 2)
+            return apply_rotary_qk(a, b, torch.complex(fre, fim).view(1, 1, N, D // 2))
+
+        qus = time_fn(torch, lambda: ops.qk_norm_rotary(xq, xk, wq, wk, 1e-6, 1e-6, D, fre, fim), 10, 2) * 1e3
+        qtus = time_fn(torch, qk_torch, 3, 1) * 1e3
+        qk_bytes = 4 * xq.numel() * 2 + 2 * fre.numel() * 4
+        out["qk_norm_rotary"] = {"fused_us": round(qus, 1), "torch_ops_us": round(qtus, 1),
+                                 "hbm_gbs": round(qk_bytes / (qus * 1e-6) / 1e9, 1),
+                                 "note": "RMSNorm over C=1536 + rotary of q and k, [2, 32760, 1536] bf16"}
+        del xq, xk
         out["wan_layer_with_compensation"] = {
             "fused_ms": round(fms, 4), "unfused_ms": round(ums, 4),
             "mean_pool_tokens_us": round(pus, 1),

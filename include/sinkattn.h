@@ -127,6 +127,28 @@ int sinkattn_mean_pool_tokens(const void* x, int dtype, int64_t B, int64_t H, in
                               void* stream);
 
 /* ------------------------------------------------------------------------------------
+ * QK-norm + rotary embedding of Q and K in one pass.
+ *
+ * Replaces `apply_fast_qk_norm` + `apply_fast_rotary_qk` (wanx/runtime/fast_misc.py:
+ * 216-234,834-864; their Triton kernels :308-340 and :432-500) and the norm + rotary of
+ * `prepare_zimage_attention_tensors` (zimg/runtime/modify_zimage.py:8-43).  For each of
+ * `rows` rows of C channels (row r at in + r*in_row_stride):
+ *     rstd = 1/sqrt(sum(x^2)/C + eps);  y = dtype(x * rstd * w)        (w fp32 [C])
+ *     then every channel pair (2i, 2i+1) of every D-channel head is rotated by the table
+ *     row t = (r / rows_per_pos) % freq_rows:  (y0*re[t,i] - y1*im[t,i], y0*im[t,i] + y1*re[t,i])
+ * freq_real/freq_imag fp32 [freq_rows, D/2] (both NULL: no rotation).  Wan: rows = B*N,
+ * C = H*D, rows_per_pos = 1, freq_rows = N.  Z-Image: rows = B*N*H, C = D,
+ * rows_per_pos = H, freq_rows = B*N.  Outputs written with out_row_stride; in-place is
+ * allowed.  C <= 8192 (16-bit) / 4096 (f32) elements; D a multiple of 16 bytes.
+ * ---------------------------------------------------------------------------------- */
+int sinkattn_qk_norm_rotary(const void* q_in, const void* k_in, int dtype, int64_t rows,
+                            int64_t C, int64_t D, int64_t in_row_stride,
+                            const float* wq, const float* wk, float eps_q, float eps_k,
+                            const float* freq_real, const float* freq_imag,
+                            int64_t rows_per_pos, int64_t freq_rows,
+                            void* q_out, void* k_out, int64_t out_row_stride, void* stream);
+
+/* ------------------------------------------------------------------------------------
  * LSE mix of two attention outputs.
  *
  * Replaces `_mix_attention_outputs` (sinkattention/sparse_attention.py:898-919) for

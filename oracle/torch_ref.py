@@ -306,3 +306,25 @@ def mean_pool_tokens(x: torch.Tensor, gap: int, prefix: int = 0) -> torch.Tensor
             total = total + missing * body[:, :, m - 1]
         groups.append(total / gap)
     return torch.cat([x[:, :, :prefix], torch.stack(groups, dim=2)], dim=2)
+
+
+# ---------------------------------------------------------------------------------------
+# QK-norm and rotary embedding in front of the attention:
+#   wanx/runtime/fast_misc.py:308-340 (_rms_norm_fwd_fused), 432-500 (_rotary_qk_fwd_fused),
+#   182-192 (_torch_real_apply_rotary_emb); zimg/runtime/modify_zimage.py:8-43.
+# ---------------------------------------------------------------------------------------
+def rms_norm_rows(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """fp32 on CPU: x * (1 / sqrt(mean(x^2) + eps)) * w over the last dim."""
+    x = x.detach().cpu().float()
+    var = (x * x).sum(-1, keepdim=True) / x.size(-1)
+    return x * (1.0 / torch.sqrt(var + eps)) * w.detach().cpu().float()
+
+
+def rotate_pairs(y: torch.Tensor, real: torch.Tensor, imag: torch.Tensor) -> torch.Tensor:
+    """Channel pairs (2i, 2i+1) of the last dim rotated by (real[..., i], imag[..., i]):
+    (y0*re - y1*im, y0*im + y1*re); real/imag broadcast against y[..., ::2]."""
+    y0, y1 = y[..., 0::2], y[..., 1::2]
+    out = torch.empty_like(y)
+    out[..., 0::2] = y0 * real - y1 * imag
+    out[..., 1::2] = y0 * imag + y1 * real
+    return out

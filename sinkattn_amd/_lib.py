@@ -49,6 +49,11 @@ SIGNATURES = {
         ctypes.c_int,
         [_c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64_4, _c_i64, _c_i64, _c_p, _c_i64_4, _c_p],
     ),
+    "sinkattn_qk_norm_rotary": (
+        ctypes.c_int,
+        [_c_p, _c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, ctypes.c_float, ctypes.c_float,
+         _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p],
+    ),
     "sinkattn_lse_mix": (
         ctypes.c_int,
         [_c_p, _c_i64_4, _c_p, _c_i64_3, _c_p, _c_i64_4, _c_p, _c_i64_3, ctypes.c_int, _c_i64, _c_i64,
@@ -101,7 +106,11 @@ def load_library() -> ctypes.CDLL:
         )
     lib = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_LOCAL)
     for name, (res, args) in SIGNATURES.items():
-        fn = getattr(lib, name)
+        try:
+            fn = getattr(lib, name)
+        except AttributeError as exc:
+            raise ImportError(f"{LIB_PATH} lacks {name}: it predates this source tree; rebuild it with "
+                              "`python -m sinkattn_amd.build`") from exc
         fn.restype = res
         fn.argtypes = args
     _LIB = lib

@@ -25,6 +25,7 @@ SOURCES = [
     "pooling.hip",
     "coverage_mask.hip",
     "compensation.hip",
+    "qk_prep.hip",
     "capi.cpp",
 ]
 

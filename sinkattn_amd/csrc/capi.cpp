@@ -245,6 +245,49 @@ int sinkattn_mean_pool_tokens(const void* x, int dtype, int64_t B, int64_t H, in
   return hip_status(sa::launch_mean_pool_tokens(a, dtype, (hipStream_t)stream), "mean_pool_tokens launch");
 }
 
+int sinkattn_qk_norm_rotary(const void* q_in, const void* k_in, int dtype, int64_t rows, int64_t C,
+                            int64_t D, int64_t in_row_stride, const float* wq, const float* wk, float eps_q,
+                            float eps_k, const float* freq_real, const float* freq_imag, int64_t rows_per_pos,
+                            int64_t freq_rows, void* q_out, void* k_out, int64_t out_row_stride, void* stream) {
+  if (!valid_dtype(dtype)) return fail("qk_norm_rotary: unsupported dtype %d", dtype);
+  const int64_t epc = dtype == SINKATTN_F32 ? 4 : 8;
+  if (rows < 0 || C <= 0 || D <= 0 || C % D != 0 || D % epc != 0 || C / epc > 1024)
+    return fail("qk_norm_rotary: C=%lld, D=%lld unsupported (D | C, D a multiple of %lld, C <= %lld)",
+                (long long)C, (long long)D, (long long)epc, (long long)(1024 * epc));
+  if (rows == 0) return 0;
+  if (rows_per_pos < 1 || freq_rows < 1) return fail("qk_norm_rotary: bad rotation table indexing");
+  if (in_row_stride < C || out_row_stride < C || in_row_stride % epc || out_row_stride % epc)
+    return fail("qk_norm_rotary: row strides must be >= C and multiples of 16 bytes");
+  if ((rows + 3) / 4 > kMaxInt) return fail("qk_norm_rotary: too many rows");
+  const void* ptrs[6] = {q_in, k_in, q_out, k_out, wq, wk};
+  for (const void* p : ptrs)
+    if (p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 != 0)
+      return fail("qk_norm_rotary: tensors and weights must be non-null and 16-byte aligned");
+  if ((freq_real == nullptr) != (freq_imag == nullptr)) return fail("qk_norm_rotary: give both or neither table");
+  if (freq_real != nullptr && (reinterpret_cast<uintptr_t>(freq_real) % 16 != 0 ||
+                               reinterpret_cast<uintptr_t>(freq_imag) % 16 != 0))
+    return fail("qk_norm_rotary: rotation tables must be 16-byte aligned");
+  sa::QkPrepArgs a{};
+  a.q_in = q_in;
+  a.k_in = k_in;
+  a.q_out = q_out;
+  a.k_out = k_out;
+  a.in_stride = in_row_stride;
+  a.out_stride = out_row_stride;
+  a.wq = wq;
+  a.wk = wk;
+  a.eps_q = eps_q;
+  a.eps_k = eps_k;
+  a.freq_real = freq_real;
+  a.freq_imag = freq_imag;
+  a.rows = rows;
+  a.rows_per_pos = rows_per_pos;
+  a.freq_rows = freq_rows;
+  a.C = (int)C;
+  a.D = (int)D;
+  return hip_status(sa::launch_qk_prep(a, dtype, (hipStream_t)stream), "qk_norm_rotary launch");
+}
+
 int sinkattn_lse_mix(const void* sink_out, const int64_t sink_strides[4], const void* sink_lse,
                      const int64_t sink_lse_strides[3], const void* dyn_out, const int64_t dyn_strides[4],
                      const void* dyn_lse, const int64_t dyn_lse_strides[3], int dtype, int64_t B, int64_t H,

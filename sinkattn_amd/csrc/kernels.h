@@ -85,6 +85,23 @@ struct MixArgs {
   float log_gap;
 };
 
+// RMSNorm (weights w, eps) over rows of C channels, then rotation of the channel pairs
+// of every D-channel head by the table row (row / rows_per_pos) % freq_rows.
+struct QkPrepArgs {
+  const void* q_in;
+  const void* k_in;
+  void* q_out;
+  void* k_out;
+  int64_t in_stride, out_stride;  // elements between rows
+  const float* wq;
+  const float* wk;
+  float eps_q, eps_k;
+  const float* freq_real;  // [freq_rows, D/2] fp32, or null: no rotation
+  const float* freq_imag;
+  int64_t rows, rows_per_pos, freq_rows;
+  int C, D;
+};
+
 constexpr int kXcds = 8;  // gfx950: work-group i is dispatched to XCD i % 8
 int plan_order_slots(int rows, int nqb);
 hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream);
@@ -96,5 +113,6 @@ hipError_t launch_mean_pool(const PoolArgs& a, int dtype, int D, hipStream_t str
 hipError_t launch_coverage_mask(const MaskArgs& a, hipStream_t stream);
 hipError_t launch_mean_pool_tokens(const TokenPoolArgs& a, int dtype, hipStream_t stream);
 hipError_t launch_lse_mix(const MixArgs& a, int dtype, hipStream_t stream);
+hipError_t launch_qk_prep(const QkPrepArgs& a, int dtype, hipStream_t stream);
 
 }  // namespace sa

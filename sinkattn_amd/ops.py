@@ -282,6 +282,53 @@ def lse_mix(sink_out: torch.Tensor, sink_lse: torch.Tensor, dyn_out: torch.Tenso
     return out
 
 
+def qk_norm_rotary(q: torch.Tensor, k: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, eps_q: float,
+                   eps_k: float, head_dim: int, freq_real: Optional[torch.Tensor] = None,
+                   freq_imag: Optional[torch.Tensor] = None, rows_per_pos: int = 1,
+                   out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """RMSNorm of every row of C = q.size(-1) channels (weights wq/wk, fp32 math) and the
+    rotation of each head's channel pairs by the table row (row // rows_per_pos) %
+    freq_rows, in one kernel for q and k.  q and k are [..., C] with contiguous rows
+    (equal shapes); freq_real/freq_imag are [freq_rows, head_dim // 2] (None: no
+    rotation).  Returns new tensors of q's shape (or writes `out`)."""
+    _require_cuda("qk_norm_rotary", q, k)
+    if q.shape != k.shape or q.dtype != k.dtype:
+        raise ValueError("qk_norm_rotary: q and k must have one shape and dtype")
+    C = int(q.size(-1))
+    rows = q.numel() // max(C, 1)
+    qc, kc = q.reshape(rows, C), k.reshape(rows, C)
+    if qc.stride(1) != 1 or kc.stride(1) != 1 or qc.stride(0) != kc.stride(0):
+        qc, kc = qc.contiguous(), kc.contiguous()
+    wq32 = wq.detach().to(device=q.device, dtype=torch.float32).contiguous()
+    wk32 = wk.detach().to(device=q.device, dtype=torch.float32).contiguous()
+    if wq32.numel() != C or wk32.numel() != C:
+        raise ValueError(f"qk_norm_rotary: weights must have {C} elements")
+    if (freq_real is None) != (freq_imag is None):
+        raise ValueError("qk_norm_rotary: give both rotation tables or neither")
+    fr = fi = None
+    freq_rows = 1
+    if freq_real is not None:
+        fr = freq_real.detach().to(device=q.device, dtype=torch.float32).reshape(-1, head_dim // 2).contiguous()
+        fi = freq_imag.detach().to(device=q.device, dtype=torch.float32).reshape(-1, head_dim // 2).contiguous()
+        freq_rows = int(fr.size(0))
+    if out is None:
+        qo, ko = torch.empty_like(qc), torch.empty_like(kc)
+    else:
+        qo, ko = out[0].reshape(rows, C), out[1].reshape(rows, C)
+    L = _lib.lib()
+    with torch.cuda.device(q.device):
+        _lib.check(
+            L.sinkattn_qk_norm_rotary(
+                qc.data_ptr(), kc.data_ptr(), _lib.dtype_code(q.dtype), rows, C, int(head_dim), int(qc.stride(0)),
+                wq32.data_ptr(), wk32.data_ptr(), float(eps_q), float(eps_k), _lib.ptr(fr), _lib.ptr(fi),
+                int(rows_per_pos), freq_rows, qo.data_ptr(), ko.data_ptr(), int(qo.stride(0)),
+                _lib.stream_ptr(q.device),
+            ),
+            "qk_norm_rotary",
+        )
+    return qo.view(q.shape), ko.view(k.shape)
+
+
 def block_mass_scores(q: torch.Tensor, k: torch.Tensor, block_size: int = 128,
                       scale: Optional[float] = None) -> torch.Tensor:
     """Exact per-(q-block, k-block) mean softmax mass, fp32 [B, H, nqb, nkb]."""

@@ -7,8 +7,9 @@ two installers.  The attention math goes through `sinkattn_amd.sparse_attention`
 (block-sparse HIP kernel, compensation branch, LSE mix), so a model patched with these
 installers runs the MI355X kernels end to end.
 
-QK-norm and rotary embedding are the model's own ops in front of the hot path; they are
-applied with plain torch here (the reference's fallback arithmetic,
+QK-norm and rotary embedding are the model's own ops in front of the hot path: one
+fused kernel (`ops.qk_norm_rotary`) for weighted RMSNorms and complex or (cos, sin)
+tables, otherwise plain torch (the reference's fallback arithmetic,
 `wanx/runtime/fast_misc.py:173-192,834-864`).
 """
 from __future__ import annotations
@@ -260,6 +261,68 @@ def apply_rotary_qk(query: torch.Tensor, key: torch.Tensor, freqs) -> tuple[torc
     return _rotate(query, freqs), _rotate(key, freqs)
 
 
+# QK-norm + rotary as one kernel (sinkattn_qk_norm_rotary) whenever the layer's norms are
+# weighted RMSNorms and the rotary table is given as complex values or (cos, sin).
+FUSE_QK_PREP = True
+
+
+def rms_norm_params(norm) -> Optional[tuple]:
+    """(weight, eps) of a norm module the fused kernel restates: a weight, a numeric eps,
+    no bias and not a LayerNorm (the same test as fast_misc.py:839-852), else None."""
+    if norm is None:
+        return None
+    w, eps = getattr(norm, "weight", None), getattr(norm, "eps", None)
+    if w is None or eps is None or getattr(norm, "bias", None) is not None:
+        return None
+    if "layernorm" in type(norm).__name__.lower():
+        return None
+    return w, float(eps)
+
+
+def rotary_tables_2d(freqs, n: int, head_dim: int) -> Optional[tuple]:
+    """(real, imag) fp32 [rows, head_dim/2] of a complex table or of Wan's (cos, sin)
+    per-channel tables, or None for any other form."""
+    half = head_dim // 2
+    if isinstance(freqs, torch.Tensor) and torch.is_complex(freqs):
+        if freqs.numel() % half != 0:
+            return None
+        return freqs.real.reshape(-1, half), freqs.imag.reshape(-1, half)
+    if isinstance(freqs, (tuple, list)) and len(freqs) == 2:
+        cos, sin = freqs
+        if cos.dim() != 4 or cos.size(-1) != head_dim:
+            return None
+        if cos.size(1) == n:  # [1, N, 1, D]
+            cos, sin = cos[0, :, 0], sin[0, :, 0]
+        elif cos.size(2) == n:  # [1, 1, N, D]
+            cos, sin = cos[0, 0], sin[0, 0]
+        else:
+            return None
+        return cos[..., 0::2].reshape(-1, half), sin[..., 1::2].reshape(-1, half)
+    return None
+
+
+def _fused_qk_prep(attn, query: torch.Tensor, key: torch.Tensor, rotary_emb):
+    """Q/K `[B, N, C]` after norm and rotary from one kernel, or None when the layer does
+    not fit it (the torch path then runs)."""
+    if not (FUSE_QK_PREP and query.is_cuda and query.dim() == 3 and query.shape == key.shape
+            and query.dtype in (torch.bfloat16, torch.float16) and key.dtype == query.dtype):
+        return None
+    pq, pk = rms_norm_params(getattr(attn, "norm_q", None)), rms_norm_params(getattr(attn, "norm_k", None))
+    if pq is None or pk is None:
+        return None
+    C = int(query.size(-1))
+    if C % int(attn.heads) != 0 or pq[0].numel() != C or pk[0].numel() != C:
+        return None
+    D = C // int(attn.heads)
+    tables = None
+    if rotary_emb is not None:
+        tables = rotary_tables_2d(rotary_emb, int(query.size(1)), D)
+        if tables is None or tables[0].size(0) != int(query.size(1)):
+            return None
+    fr, fi = tables if tables is not None else (None, None)
+    return ops.qk_norm_rotary(query, key, pq[0], pk[0], pq[1], pk[1], D, fr, fi, rows_per_pos=1)
+
+
 def _prepare_attention_tensors(attn, hidden_states: torch.Tensor,
                                encoder_hidden_states: Optional[torch.Tensor] = None,
                                rotary_emb=None):
@@ -276,6 +339,11 @@ def _prepare_attention_tensors(attn, hidden_states: torch.Tensor,
     key = attn.to_k(encoder_hidden_states)
     value = attn.to_v(encoder_hidden_states)
     on = timing is not None and getattr(timing, "is_enabled", False)
+    with (timing.section("qk_prep") if on else nullcontext()):
+        fused = _fused_qk_prep(attn, query, key, rotary_emb)
+    if fused is not None:
+        query, key, value = (t.unflatten(2, (attn.heads, -1)).transpose(1, 2) for t in (*fused, value))
+        return query, key, value, img_ctx
     with (timing.section("qk_norm") if on else nullcontext()):
         query, key = apply_qk_norm(attn, query, key)
     query, key, value = (t.unflatten(2, (attn.heads, -1)).transpose(1, 2) for t in (query, key, value))

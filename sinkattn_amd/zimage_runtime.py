@@ -212,11 +212,41 @@ def apply_zimage_rotary_emb(x_in: torch.Tensor, freqs_cis: torch.Tensor) -> torc
     return torch.stack((x1 * c - x2 * s, x1 * s + x2 * c), dim=-1).flatten(-2).type_as(x_in)
 
 
+# Per-head QK-norm + rotary as one kernel when both norms are weighted RMSNorms.
+FUSE_QK_PREP = True
+
+
+def _fused_qk_prep(attn: Any, q: torch.Tensor, k: torch.Tensor, freqs_cis: Optional[torch.Tensor]):
+    """q, k `[B, N, H, d]` normed and rotated by `ops.qk_norm_rotary` (rows = B*N*H of d
+    channels, one table row per (b, n) position), or None when the layer does not fit."""
+    from .wan_runtime import rms_norm_params
+    if not (FUSE_QK_PREP and q.is_cuda and q.dtype in (torch.bfloat16, torch.float16) and q.dim() == 4):
+        return None
+    pq, pk = rms_norm_params(attn.norm_q), rms_norm_params(attn.norm_k)
+    D = int(q.size(-1))
+    if pq is None or pk is None or pq[0].numel() != D or pk[0].numel() != D:
+        return None
+    fr = fi = None
+    if freqs_cis is not None:
+        if not torch.is_complex(freqs_cis) or freqs_cis.size(-1) != D // 2:
+            return None
+        f = freqs_cis.reshape(-1, D // 2)
+        B, N = int(q.size(0)), int(q.size(1))
+        if f.size(0) not in (N, B * N):
+            return None
+        fr, fi = f.real, f.imag
+    return ops.qk_norm_rotary(q, k, pq[0], pk[0], pq[1], pk[1], D, fr, fi, rows_per_pos=int(q.size(2)))
+
+
 def prepare_zimage_attention_tensors(attn: Any, hidden_states: torch.Tensor, *,
                                      freqs_cis: Optional[torch.Tensor] = None):
     """Q/K/V `[B, N, H, d]`: projections, head split, optional norms and rotary, all cast
-    to V's dtype (zimg/runtime/modify_zimage.py:16-43)."""
+    to V's dtype (zimg/runtime/modify_zimage.py:16-43); norm + rotary as one kernel when
+    the layer fits it."""
     q, k, v = (proj(hidden_states).unflatten(-1, (attn.heads, -1)) for proj in (attn.to_q, attn.to_k, attn.to_v))
+    fused = _fused_qk_prep(attn, q, k, freqs_cis) if q.dtype == v.dtype else None
+    if fused is not None:
+        return fused[0], fused[1], v
     if attn.norm_q is not None:
         q = attn.norm_q(q)
     if attn.norm_k is not None:

@@ -309,3 +309,48 @@ def test_zimage_calibrator_accumulation_math():
     assert torch.allclose(mean[:, 1, 1], a[:, 1, 1])
     assert torch.allclose(mean[:, 2, 2], (a[:, 2, 2] + b[:, 1, 1]) / 2)
     assert cal.score_counts[0] == 2
+
+
+# --- QK-norm / rotary: oracle pins and host-side dispatch ---------------------------------------
+def test_rms_norm_and_rotation_oracle_pins():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(7, 64, generator=g)
+    w = torch.rand(64, generator=g) + 0.5
+    y = torch_ref.rms_norm_rows(x, w, 1e-6)
+    # unit RMS after dividing out w; invariant to a positive scale of x (eps aside)
+    assert torch.allclose(((y / w) ** 2).mean(-1), torch.ones(7), atol=1e-5)
+    assert torch.allclose(torch_ref.rms_norm_rows(3.5 * x, w, 0.0), torch_ref.rms_norm_rows(x, w, 0.0), atol=1e-6)
+    # constant row c: y = w * c / sqrt(c^2 + eps)
+    c = torch.full((1, 64), 0.25)
+    assert torch.allclose(torch_ref.rms_norm_rows(c, w, 1e-2), w * 0.25 / math.sqrt(0.0625 + 1e-2), atol=1e-7)
+    # rotation: identity at angle 0, (a, b) -> (-b, a) at pi/2, pair norms kept, = complex product
+    z = torch.randn(3, 5, 16, generator=g, dtype=torch.float64)
+    assert torch.equal(torch_ref.rotate_pairs(z, torch.ones(8, dtype=torch.float64), torch.zeros(8, dtype=torch.float64)), z)
+    r90 = torch_ref.rotate_pairs(z, torch.zeros(8, dtype=torch.float64), torch.ones(8, dtype=torch.float64))
+    assert torch.equal(r90[..., 0::2], -z[..., 1::2]) and torch.equal(r90[..., 1::2], z[..., 0::2])
+    ang = torch.randn(5, 8, generator=g, dtype=torch.float64)
+    rot = torch_ref.rotate_pairs(z, torch.cos(ang), torch.sin(ang))
+    norms = lambda t: t[..., 0::2] ** 2 + t[..., 1::2] ** 2
+    assert torch.allclose(norms(rot), norms(z))
+    cz = torch.view_as_complex(z.reshape(3, 5, 8, 2).contiguous()) * torch.polar(torch.ones_like(ang), ang)
+    assert torch.allclose(rot, torch.view_as_real(cz).reshape(3, 5, 16))
+
+
+def test_qk_prep_dispatch_helpers():
+    n = nn.RMSNorm(128, eps=1e-6)
+    w, eps = wr.rms_norm_params(n)
+    assert w is n.weight and eps == 1e-6
+    assert wr.rms_norm_params(nn.RMSNorm(128)) is None          # eps None: module path
+    assert wr.rms_norm_params(nn.LayerNorm(128)) is None        # has a bias / is a LayerNorm
+    assert wr.rms_norm_params(nn.RMSNorm(128, eps=1e-6, elementwise_affine=False)) is None
+    assert wr.rms_norm_params(None) is None
+    N, D = 6, 8
+    ang = torch.randn(N, D // 2, dtype=torch.float64)
+    c = torch.polar(torch.ones_like(ang), ang).to(torch.complex64)
+    re, im = wr.rotary_tables_2d(c.view(1, 1, N, D // 2), N, D)
+    assert torch.equal(re, c.real) and torch.equal(im, c.imag)
+    cos = torch.cos(ang).float().repeat_interleave(2, -1).view(1, N, 1, D)
+    sin = torch.sin(ang).float().repeat_interleave(2, -1).view(1, N, 1, D)
+    re2, im2 = wr.rotary_tables_2d((cos, sin), N, D)
+    assert torch.allclose(re2, c.real) and torch.allclose(im2, c.imag)
+    assert wr.rotary_tables_2d(torch.randn(N, D), N, D) is None
