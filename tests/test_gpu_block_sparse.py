@@ -204,3 +204,42 @@ def test_wan_config2_full_size_rows_subsampled():
     torch.cuda.synchronize()
     rows = torch.cat([torch.randperm(N - 120, generator=g)[:40], torch.arange(N - 8, N)]).sort().values
     _check(out, lse[..., 0], q, k, v, mask, rows=rows)
+
+
+@pytest.mark.slow
+def test_zimage_config4_full_size_rows_subsampled():
+    # B=1, H=30, N=16896 (16384 image + 512 text tokens), bf16, the last
+    # 512 keys x4; mask [1, 30, 132, 132] with the required prefix rows/cols 0-3 (what the
+    # coverage builder adds for text_length=512), the diagonal and a seeded 15% remainder.
+    B, H, N = 1, 30, 16896
+    q, k, v = _inputs(B, H, N, N, 128, torch.bfloat16, seed=30)
+    k[:, :, N - 512:] *= 4.0
+    mask = _random_mask(B, H, 132, 132, 0.15, seed=31)
+    mask[..., :4] = True
+    mask[..., :4, :] = True
+    out, lse = sa._block_sparse_attn(q, k, v, mask)
+    torch.cuda.synchronize()
+    g = torch.Generator().manual_seed(32)
+    rows = torch.cat([torch.arange(0, 8), torch.randperm(N, generator=g)[:40], torch.arange(N - 8, N)])
+    _check(out, lse[..., 0], q, k, v, mask, rows=rows.unique())
+
+
+@pytest.mark.slow
+def test_config5_mixed_head_densities_rows_subsampled():
+    # BASELINE config 5 shape: C2-sized calls with per-head densities drawn from [5%, 60%]
+    # and one fully dense head; the launch order balances such heads across XCDs.
+    B, H, N = 2, 12, 32760
+    q, k, v = _inputs(B, H, N, N, 128, torch.bfloat16, seed=40)
+    g = torch.Generator().manual_seed(41)
+    dens = 0.05 + 0.55 * torch.rand(H, generator=g)
+    m = torch.rand(B, H, 256, 256, generator=g) < dens.view(1, H, 1, 1)
+    m[:, 5] = True
+    d = torch.arange(256)
+    m[:, :, d, d] = True
+    mask = m.cuda()
+    plan = ops.block_sparse_plan(mask)
+    _check_order(plan, plan.counts.cpu(), B * H, 256)
+    out, lse = ops.block_sparse_attention(q, k, v, plan)
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.randperm(N - 120, generator=g)[:24], torch.arange(N - 4, N)]).sort().values
+    _check(out, lse, q, k, v, mask, rows=rows)
