@@ -260,6 +260,10 @@ def main():
                           "mfma_frac": round(pool_flops / (pms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
                           "traffic": traffic_bytes("pool"),
                           "kernel": "sa::block_mass_persistent_kernel<0> (bf16)"}
+        # the "triton" pooling mode (attn_with_pooling's row-normalised max-pool map)
+        mms = time_fn(torch, lambda: ops.max_pool_scores(q, k, 1.0 / math.sqrt(D)), 3, 1)
+        out["pooling"]["max_pool_ms"] = round(mms, 3)
+        out["pooling"]["max_pool_tflops"] = round(pool_flops / (mms * 1e-3) / 1e12, 2)
         # the full Wan layer call with the default compensation branch (pooled_kv, gap 30,
         # adaptive mix): fused kernel vs the reference's three steps on this build's kernels
         from sinkattn_amd import sparse_attention as sa

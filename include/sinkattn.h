@@ -199,13 +199,18 @@ int sinkattn_block_mass_pool(const void* q, const void* k, int dtype,
  * Po is written in q.dtype (bf16 or f16) as [B,H,nd,nd] contiguous.  kv head of query
  * head h is h / (H / Hk).  causal restricts row qb to kb <= qb and adds -1e6 to the
  * raw scores above the diagonal of the diagonal tile, as the reference does.  Keys and
- * rows >= N are excluded (the reference leaves ragged N undefined).  block_size = 128.
+ * rows >= N are excluded (the reference leaves ragged N undefined).  block_size = 128,
+ * D = 128, nd <= 1024.  `workspace` is a device buffer of at least
+ * sinkattn_max_pool_workspace_bytes(...) bytes (per-(row, key-block) maxima of the
+ * rows in flight); calls that share one workspace must be ordered on one stream.
  * ---------------------------------------------------------------------------------- */
+size_t sinkattn_max_pool_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t block_size,
+                                         int dtype);
 int sinkattn_max_pool(const void* q, const void* k, int dtype,
                       int64_t B, int64_t H, int64_t Hk, int64_t N, int64_t D,
                       const int64_t q_strides[4], const int64_t k_strides[4],
                       int64_t block_size, float sm_scale, int causal, void* po,
-                      void* stream);
+                      void* workspace, void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Mean-pooled block scores ("mean" pooling mode).

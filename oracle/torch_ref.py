@@ -78,8 +78,13 @@ def exact_block_mass_fp64(q: torch.Tensor, k: torch.Tensor, block_size: int = 12
 # row sum rounded to q.dtype, the division rounded to q.dtype.
 # ---------------------------------------------------------------------------------------
 def max_pool_map(q: torch.Tensor, k: torch.Tensor, sm_scale: float, block_size: int = 128,
-                 causal: bool = False, exact: bool = False) -> torch.Tensor:
-    """exact=True evaluates the formula in float64 without any rounding."""
+                 causal: bool = False, exact: bool = False, query_blocks=None) -> torch.Tensor:
+    """exact=True evaluates the formula in float64 without any rounding.
+
+    query_blocks (optional): the query-block indices to evaluate, in order; the result
+    then holds those rows of the map only.  Each query block is computed on its own
+    (rows of the map are independent), so long sequences fit in memory.
+    """
     dt = q.dtype
     work = torch.float64 if exact else torch.float32
     q = q.detach().cpu().to(work)
@@ -88,32 +93,31 @@ def max_pool_map(q: torch.Tensor, k: torch.Tensor, sm_scale: float, block_size: 
     Hk = k.size(1)
     if Hk != H:
         k = k.repeat_interleave(H // Hk, dim=1)
+    kt = k.transpose(-1, -2)
     nd = _cdiv(N, block_size)
     qk_scale = torch.tensor(sm_scale, dtype=torch.float32) * torch.tensor(1.44269504, dtype=torch.float32)
     qk_scale = float(qk_scale) if not exact else float(sm_scale) * 1.44269504
-    s = torch.matmul(q, k.transpose(-1, -2))  # raw qk
-    if causal:
-        tri = torch.arange(N).view(-1, 1) < torch.arange(N).view(1, -1)
-        # only the diagonal tile gets the additive -1e6; off-diagonal tiles above it are
-        # never visited
-        qb_idx = torch.arange(N) // block_size
-        same = qb_idx.view(-1, 1) == qb_idx.view(1, -1)
-        s = s + torch.where(tri & same, torch.tensor(-1.0e6, dtype=work), torch.tensor(0.0, dtype=work))
-    s = F.pad(s, (0, nd * block_size - N), value=float("-inf"))
-    bmax = s.view(B, H, N, nd, block_size).amax(-1) * qk_scale  # [B,H,N,nd]
-    if causal:
-        kbi = torch.arange(nd).view(1, -1)
-        rowb = (torch.arange(N) // block_size).view(-1, 1)
-        bmax = bmax.masked_fill(kbi > rowb, float("-inf"))
-    m = bmax.amax(-1, keepdim=True)
-    r = bmax if exact else bmax.to(dt).to(work)
-    e = torch.exp2(r - m)
-    po = torch.zeros(B, H, nd, nd, dtype=work)
-    for qbi in range(nd):
-        rows = e[:, :, qbi * block_size:min((qbi + 1) * block_size, N), :]
-        po[:, :, qbi] = rows.amax(dim=2)
-    if causal:
-        po = po.masked_fill(torch.arange(nd).view(1, -1) > torch.arange(nd).view(-1, 1), 0.0)
+    qbs = list(range(nd)) if query_blocks is None else [int(x) for x in query_blocks]
+    po = torch.zeros(B, H, len(qbs), nd, dtype=work)
+    cols = torch.arange(N)
+    for i, qbi in enumerate(qbs):
+        r0, r1 = qbi * block_size, min((qbi + 1) * block_size, N)
+        s = torch.matmul(q[:, :, r0:r1], kt)  # raw qk, [B,H,rows,N]
+        if causal:
+            # only the diagonal tile gets the additive -1e6; tiles right of it are never
+            # visited
+            rows = torch.arange(r0, r1).view(-1, 1)
+            above = (cols.view(1, -1) > rows) & (cols.view(1, -1) // block_size == qbi)
+            s = s + torch.where(above, torch.tensor(-1.0e6, dtype=work), torch.tensor(0.0, dtype=work))
+        s = F.pad(s, (0, nd * block_size - N), value=float("-inf"))
+        bmax = s.view(B, H, r1 - r0, nd, block_size).amax(-1) * qk_scale  # [B,H,rows,nd]
+        if causal:
+            bmax[..., qbi + 1:] = float("-inf")
+        m = bmax.amax(-1, keepdim=True)
+        r = bmax if exact else bmax.to(dt).to(work)
+        po[:, :, i] = torch.exp2(r - m).amax(dim=2)
+        if causal:
+            po[:, :, i, qbi + 1:] = 0.0
     if exact:
         return po / po.sum(-1, keepdim=True)
     po = po.to(dt)

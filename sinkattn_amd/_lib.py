@@ -67,10 +67,13 @@ SIGNATURES = {
         [_c_p, _c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64_4, _c_i64_4,
          _c_i64, ctypes.c_float, _c_p, _c_p, _c_p],
     ),
+    "sinkattn_max_pool_workspace_bytes": (
+        ctypes.c_size_t, [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int],
+    ),
     "sinkattn_max_pool": (
         ctypes.c_int,
         [_c_p, _c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64_4, _c_i64_4,
-         _c_i64, ctypes.c_float, ctypes.c_int, _c_p, _c_p],
+         _c_i64, ctypes.c_float, ctypes.c_int, _c_p, _c_p, _c_p],
     ),
     "sinkattn_mean_pool_workspace_bytes": (
         ctypes.c_size_t, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64],
@@ -95,6 +98,11 @@ class SinkAttnError(RuntimeError):
     """A libsinkattn entry point returned a non-zero status."""
 
 
+# Version of the entry-point signatures declared in include/sinkattn.h (raised whenever an
+# existing signature changes).
+ABI_VERSION = 2
+
+
 def load_library() -> ctypes.CDLL:
     """Load libsinkattn.so and declare its signatures (no GPU needed)."""
     global _LIB
@@ -113,6 +121,9 @@ def load_library() -> ctypes.CDLL:
                               "`python -m sinkattn_amd.build`") from exc
         fn.restype = res
         fn.argtypes = args
+    if lib.sinkattn_abi_version() != ABI_VERSION:
+        raise ImportError(f"{LIB_PATH} has ABI version {lib.sinkattn_abi_version()}, this source tree "
+                          f"expects {ABI_VERSION}; rebuild it with `python -m sinkattn_amd.build`")
     _LIB = lib
     return lib
 

@@ -55,7 +55,7 @@ extern "C" {
 
 const char* sinkattn_last_error(void) { return g_last_error.c_str(); }
 
-int sinkattn_abi_version(void) { return 1; }
+int sinkattn_abi_version(void) { return 2; }
 
 int64_t sinkattn_block_sparse_order_slots(int64_t B, int64_t H, int64_t nqb) {
   if (B <= 0 || H <= 0 || nqb <= 0 || B * H * nqb > kMaxInt) return 0;
@@ -390,19 +390,30 @@ int sinkattn_block_mass_pool(const void* q, const void* k, int dtype, int64_t B,
   return hip_status(sa::launch_block_mass_pool(a, dtype, (int)D, (hipStream_t)stream), "pool launch");
 }
 
+size_t sinkattn_max_pool_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t block_size, int dtype) {
+  if (dtype == SINKATTN_F32 || block_size <= 0) return 0;
+  return sinkattn_block_mass_pool_workspace_bytes(B, H, N, N, block_size, dtype);
+}
+
 int sinkattn_max_pool(const void* q, const void* k, int dtype, int64_t B, int64_t H, int64_t Hk,
                       int64_t N, int64_t D, const int64_t q_strides[4], const int64_t k_strides[4],
-                      int64_t block_size, float sm_scale, int causal, void* po, void* stream) {
+                      int64_t block_size, float sm_scale, int causal, void* po, void* workspace,
+                      void* stream) {
   sa::PoolArgs a{};
   if (dtype == SINKATTN_F32) return fail("max_pool: q.dtype must be bf16 or f16");
   int rc = fill_pool_args(a, "max_pool", q, k, dtype, B, H, Hk, N, N, D, q_strides, k_strides,
                           block_size);
   if (rc != 0) return rc;
-  if (a.nkb > 256) return fail("max_pool: %d key blocks exceed the supported 256", a.nkb);
+  if (a.nkb > 1024) return fail("max_pool: %d key blocks exceed the supported 1024", a.nkb);
+  if (B * H * N == 0) return 0;
   if (po == nullptr) return fail("max_pool: null output");
+  if (workspace == nullptr) return fail("max_pool: null workspace (see sinkattn_max_pool_workspace_bytes)");
+  if (k_strides[2] < D || N * k_strides[2] * 2 >= (int64_t)1 << 31)
+    return fail("max_pool: k row stride below the head dim or one head of k over 2 GiB");
   a.scale = sm_scale;
   a.causal = causal ? 1 : 0;
   a.out = po;
+  a.ws = static_cast<float*>(workspace);
   return hip_status(sa::launch_max_pool(a, dtype, (int)D, (hipStream_t)stream), "max_pool launch");
 }
 

@@ -24,94 +24,6 @@ namespace sa {
 constexpr float kRescaleMargin = 8.f;
 
 // ------------------------------------------------------------------------------------
-// Exact block mass, 16-bit inputs (exact products on the bf16/f16 matrix cores).
-// ------------------------------------------------------------------------------------
-template <int IT, int CT, int NKBMAX>
-__global__ __launch_bounds__(256) void block_mass_kernel(PoolArgs a) {
-  constexpr int D = 128;
-  constexpr int ES = ElemSize<IT>::value;
-  constexpr int KC = D / 8;
-  __shared__ u32x4 lds_k[128 * KC];           // 32 KB; reused for 1/L at the end
-  __shared__ float sums[128 * NKBMAX];        // per-(row, key-block) partial mass
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int hl = lane >> 5, l32 = lane & 31;
-  const int qb = blockIdx.x;
-  const int bh = blockIdx.y;
-  const int b = bh / a.H, h = bh - b * a.H;
-  const int nkb = a.nkb;
-
-  const char* qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * ES;
-  const char* kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)h * a.ks[1]) * ES;
-
-  const int r = wave * 32 + l32;  // row within the q-block
-  const int qrow = qb * 128 + r;
-  u32x4 qf[D / 16];
-  load_q_operand<IT, CT, D>(qf, qbase, a.qs[2], qrow, a.Nq, hl);
-
-  const int prow = k_row_perm(l32);
-  const int fk = k_swz(prow);
-  const float c = a.scale * kLog2e;
-  float m_ref = neg_inf();
-  float* my = sums + r * NKBMAX;
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int key0 = kb * 128;
-    __syncthreads();
-    stage_k_tile<IT, CT, D, 256>(lds_k, kbase, a.ks[2], key0, a.Nk, tid);
-    __syncthreads();
-    f32x16 s[4];
-    qk_tile<CT, D>(lds_k, qf, prow, fk, hl, s);
-    if (key0 + 128 > a.Nk) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (key0 + t * 32 + tile_key(hl, j) >= a.Nk) s[t][j] = neg_inf();
-    }
-    float mx = neg_inf();
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
-    mx = fmaxf(mx, xor32(mx)) * c;
-    if (mx > m_ref + kRescaleMargin) {
-      // Move the reference maximum; rescale this row's earlier sums (the two lanes of
-      // the row split the entries by parity).
-      const float f = fast_exp2(m_ref - mx);
-      for (int j = hl; j < kb; j += 2) my[j] *= f;
-      m_ref = mx;
-    }
-    float ps = 0.f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) ps += fast_exp2(__builtin_fmaf(s[t][j], c, -m_ref));
-    ps += xor32(ps);
-    if (hl == 0) my[kb] = ps;
-  }
-  __syncthreads();
-
-  // Row totals in the (now free) K-tile storage.
-  float* row_tot = reinterpret_cast<float*>(lds_k);
-  {
-    float tot = 0.f;
-    for (int j = hl; j < nkb; j += 2) tot += my[j];
-    tot += xor32(tot);
-    if (hl == 0) row_tot[r] = tot;
-  }
-  __syncthreads();
-  const int nrows = min(128, a.Nq - qb * 128);
-  float* out = reinterpret_cast<float*>(a.out) + ((int64_t)bh * a.nqb + qb) * nkb;
-  for (int kb = tid; kb < nkb; kb += 256) {
-    float acc = 0.f;
-    for (int rr = 0; rr < nrows; ++rr) acc += sums[rr * NKBMAX + kb] / fmaxf(row_tot[rr], 1e-6f);
-    out[kb] = acc / (float)nrows;
-  }
-}
-
-// ------------------------------------------------------------------------------------
 // Exact block mass, 16-bit inputs, persistent work-groups (up to 3 per CU).
 // Each work-group walks (b, h, q-block) items; per item it streams every K tile into
 // LDS by buffer DMA (rows >= Nk read as zero and are masked), computes S^T for its 128
@@ -344,9 +256,7 @@ __global__ __launch_bounds__(256) void block_mass_f32_kernel(PoolArgs a) {
   }
 }
 
-// ------------------------------------------------------------------------------------
-// Max-pool map (16-bit inputs).
-// ------------------------------------------------------------------------------------
+// Rounding of an fp32 value to the 16-bit type CT (returned as fp32).
 template <int CT>
 __device__ __forceinline__ float round_to(float x);
 template <>
@@ -358,96 +268,127 @@ __device__ __forceinline__ float round_to<kF16>(float x) {
   return (float)(_Float16)x;
 }
 
-template <int IT, int NKBMAX>
-__global__ __launch_bounds__(256) void max_pool_kernel(PoolArgs a) {
-  constexpr int CT = IT;
-  constexpr int D = 128;
-  constexpr int ES = ElemSize<IT>::value;
-  constexpr int KC = D / 8;
-  __shared__ u32x4 lds_k[128 * KC];
-  __shared__ float rmax[128 * NKBMAX];  // q.dtype-rounded block maxima, log2 domain
-
+// ------------------------------------------------------------------------------------
+// Max-pool map, persistent form (bf16/f16): the structure of block_mass_persistent_kernel
+// (3 groups per CU, K tiles by DMA, S^T on the matrix cores) with the block maxima of each
+// row kept in the group's workspace slot ws[kb][row] instead of LDS, so three groups fit
+// a CU.  Per tile: R[r,kb] = q.dtype(max_j s * sm_scale * log2e) (raw-score maximum first,
+// then the scale, as pooling_kernel.py:39-48 does), m_r = max over kb of the unrounded
+// values.  Epilogue per kb: Po[kb] = q.dtype(max over the block's rows of
+// exp2(R[r,kb] - m_r)), then the row is normalised in q.dtype (pooling_kernel.py:65-75,
+// 243-244).  kv head = h / (H / Hk); causal restricts kb <= qb and adds -1e6 above the
+// diagonal of the diagonal tile.
+// ------------------------------------------------------------------------------------
+template <int CT>
+__global__ __launch_bounds__(256, 3) void max_pool_persistent_kernel(PoolArgs a, int items) {
+  constexpr int DS = 8;
+  __shared__ u32x4 lds_k[2048];
+  __shared__ float row_m[128];
+  __shared__ float colmax[1024];
+  __shared__ float total_sh;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, l32 = lane & 31;
-  const int qb = blockIdx.x;
-  const int bh = blockIdx.y;
-  const int b = bh / a.H, h = bh - b * a.H;
-  const int hk = h / (a.H / a.Hk);
   const int nkb = a.nkb;
-  const int kb_end = a.causal ? min(nkb, qb + 1) : nkb;
-
-  const char* qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * ES;
-  const char* kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)hk * a.ks[1]) * ES;
-
-  const int r = wave * 32 + l32;
-  const int qrow = qb * 128 + r;
-  u32x4 qf[D / 16];
-  load_q_operand<IT, CT, D>(qf, qbase, a.qs[2], qrow, a.Nq, hl);
+  float* ws = a.ws + (size_t)blockIdx.x * (size_t)nkb * 128;
+  const uint32_t kstride = (uint32_t)a.ks[2] * 2;
+  const int drow = 4 * wave + (lane >> 4);
+  const uint32_t k_off = (uint32_t)drow * kstride + (uint32_t)(((lane & 15) ^ (drow & 15)) * 16);
   const int prow = k_row_perm(l32);
-  const int fk = k_swz(prow);
+  uint32_t ka[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) ka[ds] = (uint32_t)(prow * 256 + (((2 * ds + hl) ^ (prow & 15)) * 16));
+  SA_LDS char* lk = (SA_LDS char*)lds_k;
   // The reference forms qk_scale = fp32(sm_scale) * fp32(1.44269504).
   const float qk_scale = a.scale * 1.44269504f;
-  float m = neg_inf();
-  float* my = rmax + r * NKBMAX;
+  const int r = wave * 32 + l32;
 
-  for (int kb = 0; kb < kb_end; ++kb) {
-    const int key0 = kb * 128;
-    __syncthreads();
-    stage_k_tile<IT, CT, D, 256>(lds_k, kbase, a.ks[2], key0, a.Nk, tid);
-    __syncthreads();
-    f32x16 s[4];
-    qk_tile<CT, D>(lds_k, qf, prow, fk, hl, s);
-    const bool ragged = key0 + 128 > a.Nk;
-    const bool diag = a.causal && kb == qb;
-    if (ragged || diag) {
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+    const int bh = item / a.nqb;
+    const int qb = item - bh * a.nqb;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int hk = h / (a.H / a.Hk);
+    const int kb_end = a.causal ? min(nkb, qb + 1) : nkb;
+    const char* qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * 2;
+    const char* kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)hk * a.ks[1]) * 2;
+    const int qrow = qb * 128 + r;
+    u32x4 qf[DS];
+    load_q_operand<CT, CT, 128>(qf, qbase, a.qs[2], qrow, a.Nq, hl);
+    float m = neg_inf();
+
+    for (int kb = 0; kb < kb_end; ++kb) {
+      const int key0 = kb * 128;
+      __syncthreads();  // the previous tile (or item epilogue) is done with lds_k
+      {
+        const __amdgpu_buffer_rsrc_t rs =
+            make_rsrc(kbase + (int64_t)key0 * kstride, (uint32_t)(a.Nk - key0) * kstride);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          dma16(rs, (SA_LDS void*)(lk + (256 * j + 64 * wave) * 16), k_off + (uint32_t)j * 16u * kstride);
+      }
+      __syncthreads();  // waits for this group's DMA
+      f32x16 s[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) s[t] = f32x16{};
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const u32x4 av = *(SA_LDS const u32x4*)(lk + ka[ds] + t * 8192);
+          s[t] = mfma32x32x16<CT>(av, qf[ds], s[t]);
+        }
+      const bool diag = a.causal && kb == qb;
+      if (key0 + 128 > a.Nk || diag) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int key = key0 + t * 32 + tile_key(hl, j);
+            if (diag && qrow < key) s[t][j] += -1.0e6f;
+            if (key >= a.Nk) s[t][j] = neg_inf();
+          }
+      }
+      float mx = neg_inf();
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key = key0 + t * 32 + tile_key(hl, j);
-          if (diag && qrow < key) s[t][j] += -1.0e6f;
-          if (key >= a.Nk) s[t][j] = neg_inf();
-        }
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
+      mx = fmaxf(mx, xor32(mx)) * qk_scale;
+      m = fmaxf(m, mx);
+      if (hl == 0) ws[kb * 128 + r] = round_to<CT>(mx);
     }
-    float mx = neg_inf();
+
+    // Epilogue.  Rows past the end of the sequence take no part (m = +inf gives 0).
+    const int nrows = min(128, a.Nq - qb * 128);
+    if (hl == 0) row_m[r] = (r < nrows) ? m : pos_inf();
+    __syncthreads();
+    const float m0 = row_m[lane], m1 = row_m[lane + 64];
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(ws, (uint32_t)nkb * 512u);
+    for (int kb = wave; kb < kb_end; kb += 4) {
+      // coherent (L1-bypassing) loads of values other waves of the group wrote
+      const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4), 0, 1));
+      const float x1 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4 + 256), 0, 1));
+      float v = fmaxf(fast_exp2(x0 - m0), fast_exp2(x1 - m1));
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+      for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+      if (lane == 0) colmax[kb] = round_to<CT>(v);
+    }
+    __syncthreads();
+    // Row normalisation in q.dtype: sum (fp32 accumulate, rounded), then divide.
+    if (wave == 0) {
+      float part = 0.f;
+      for (int kb = lane; kb < kb_end; kb += 64) part += colmax[kb];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
-    mx = fmaxf(mx, xor32(mx)) * qk_scale;
-    m = fmaxf(m, mx);
-    if (hl == 0) my[kb] = round_to<CT>(mx);
-  }
-  __syncthreads();
-  // m_r of every row, in the K-tile storage.
-  float* mrow = reinterpret_cast<float*>(lds_k);
-  if (hl == 0) mrow[r] = m;
-  __syncthreads();
-  const int nrows = min(128, a.Nq - qb * 128);
-  float* colmax = reinterpret_cast<float*>(lds_k) + 128;  // nkb values
-  for (int kb = tid; kb < kb_end; kb += 256) {
-    float best = 0.f;
-    for (int rr = 0; rr < nrows; ++rr) best = fmaxf(best, fast_exp2(rmax[rr * NKBMAX + kb] - mrow[rr]));
-    colmax[kb] = round_to<CT>(best);
-  }
-  __syncthreads();
-  // Row normalisation in q.dtype: sum (fp32 accumulate, rounded), then divide.
-  float* total_sh = colmax + 256;
-  if (wave == 0) {
-    float part = 0.f;
-    for (int kb = lane; kb < kb_end; kb += 64) part += colmax[kb];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
-    if (lane == 0) *total_sh = round_to<CT>(part);
-  }
-  __syncthreads();
-  const float total = *total_sh;
-  uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * a.nqb + qb) * nkb;
-  for (int kb = tid; kb < nkb; kb += 256) {
-    const float v = kb < kb_end ? colmax[kb] / total : 0.f;
-    uint32_t bits = pack2<CT>(v, 0.f) & 0xffffu;
-    out[kb] = (uint16_t)bits;
+      for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+      if (lane == 0) total_sh = round_to<CT>(part);
+    }
+    __syncthreads();
+    const float total = total_sh;
+    uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * a.nqb + qb) * nkb;
+    for (int kb = tid; kb < nkb; kb += 256) {
+      const float v = kb < kb_end ? colmax[kb] / total : 0.f;
+      out[kb] = (uint16_t)(pack2<CT>(v, 0.f) & 0xffffu);
+    }
   }
 }
 
@@ -538,14 +479,12 @@ hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream
 hipError_t launch_max_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream) {
   (void)D;
   if (a.B * a.H * a.nqb == 0) return hipSuccess;
-  const dim3 grid(a.nqb, a.B * a.H);
-  if (dtype == kBF16) {
-    if (a.nkb <= 64) max_pool_kernel<kBF16, 64><<<grid, 256, 0, stream>>>(a);
-    else max_pool_kernel<kBF16, 256><<<grid, 256, 0, stream>>>(a);
-  } else {
-    if (a.nkb <= 64) max_pool_kernel<kF16, 64><<<grid, 256, 0, stream>>>(a);
-    else max_pool_kernel<kF16, 256><<<grid, 256, 0, stream>>>(a);
-  }
+  const int items = a.B * a.H * a.nqb;
+  const int groups = min(items, block_mass_groups());
+  if (dtype == kBF16)
+    max_pool_persistent_kernel<kBF16><<<groups, 256, 0, stream>>>(a, items);
+  else
+    max_pool_persistent_kernel<kF16><<<groups, 256, 0, stream>>>(a, items);
   return hipGetLastError();
 }
 

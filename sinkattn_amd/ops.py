@@ -376,11 +376,13 @@ def max_pool_scores(q: torch.Tensor, k: torch.Tensor, sm_scale: float, block_siz
     po = torch.empty((B, H, nd, nd), dtype=q.dtype, device=q.device)
     L = _lib.lib()
     with torch.cuda.device(q.device):
+        ws_bytes = int(L.sinkattn_max_pool_workspace_bytes(B, H, N, int(block_size), dt))
+        ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=q.device) if ws_bytes else None
         _lib.check(
             L.sinkattn_max_pool(
                 qk.data_ptr(), kk.data_ptr(), dt, B, H, Hk, N, D, _lib.strides4(qk),
                 _lib.strides4(kk), int(block_size), float(sm_scale), int(bool(causal)),
-                po.data_ptr(), _lib.stream_ptr(q.device),
+                po.data_ptr(), _lib.ptr(ws), _lib.stream_ptr(q.device),
             ),
             "max_pool",
         )

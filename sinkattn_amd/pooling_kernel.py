@@ -4,7 +4,8 @@
 reference's signature and outputs (sinkattention/pooling_kernel.py:194-248): ``o`` is
 all zeros in q's dtype (the reference kernel never accumulates into it) and ``Po`` is
 the row-normalised max-pool map [B, H, nd, nd] in q's dtype.  ``Po`` comes from the
-max_pool HIP kernel, which keeps the per-(row, key-block) maxima in LDS instead of the
+max_pool HIP kernel, a persistent kernel whose work-groups each keep the per-(row,
+key-block) maxima of the one query block in flight in a workspace slot, instead of the
 reference's [B, H, N, nd] scratch tensor.
 """
 from __future__ import annotations

@@ -4,8 +4,9 @@ exact mode  vs oracle/torch_ref.exact_block_mass (fp32 restatement of
             sparse_attention.py:145-227): elementwise rtol 1e-5 (atol 1e-8); rows of the
             map sum to 1.
 max mode    vs oracle/torch_ref.max_pool_map (closed form with the reference's bf16
-            rounding points): equal, or within one bf16 ulp where a rounding boundary
-            is crossed (bit-level Triton behaviour is not pinned).
+            rounding points): at least 90% of the entries equal; the rest within 3 ulps
+            of q.dtype (an fp32-ulp difference of exp2 may flip the rounding of one
+            block value and of the row total, each by one ulp, before the division).
 mean mode   vs oracle/torch_ref.mean_pool_scores: rtol 1e-5.
 """
 import math
@@ -32,6 +33,13 @@ def _qk(B, H, Nq, Nk, dtype, seed, sinks=0, sink_scale=8.0, sink_at_end=False):
         else:
             k[:, :, :sinks] *= sink_scale
     return q.to(dtype), k.to(dtype)
+
+
+def _max_pool_close(ours, ref, dtype=torch.bfloat16, what=""):
+    u = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    diff = (ours.cpu().float() - ref.float()).abs()
+    assert (diff <= ref.float().abs() * 3 * u + 1e-30).all(), (what, diff.max().item())
+    assert (diff == 0).float().mean().item() > 0.9, what
 
 
 def _close(ours, ref):
@@ -116,14 +124,34 @@ def test_max_pool_vs_closed_form(dtype, causal):
     ours = ops.max_pool_scores(q.cuda(), k.cuda(), sm, causal=causal).cpu()
     ref = torch_ref.max_pool_map(q, k, sm, causal=causal)
     assert ours.dtype == dtype
-    diff = (ours.float() - ref.float()).abs()
-    ulp = ref.float().abs() * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10) + 1e-30
-    assert (diff <= ulp).all(), diff.max().item()
-    assert (diff == 0).float().mean().item() > 0.9
+    _max_pool_close(ours, ref, dtype)
     # the unrounded formula agrees up to the reference's own rounding of the log2-domain
     # block maxima to q.dtype (|R| ~ 40 -> bf16 ulp 0.25 -> up to 2^0.125 in the ratio)
     ex = torch_ref.max_pool_map(q, k, sm, causal=causal, exact=True)
     assert torch.allclose(ours.double(), ex, rtol=0.2, atol=1e-3)
+
+
+def test_max_pool_persistent_loop_ragged():
+    # 96 heads x 9 query blocks = 864 items: more than one item per resident work-group,
+    # so the workspace slot of a group is reused; N = 1100 leaves a ragged last block.
+    q, k = _qk(1, 96, 1100, 1100, torch.bfloat16, seed=12, sinks=3)
+    sm = 1.0 / math.sqrt(128)
+    for causal in (False, True):
+        ours = ops.max_pool_scores(q.cuda(), k.cuda(), sm, causal=causal).cpu()
+        ref = torch_ref.max_pool_map(q, k, sm, causal=causal)
+        _max_pool_close(ours, ref, what=f"causal={causal}")
+
+
+def test_max_pool_many_key_blocks():
+    # N = 40000 -> 313 key blocks per row (ragged 64); three query blocks are checked
+    # against the closed form.
+    q, k = _qk(1, 1, 40000, 40000, torch.bfloat16, seed=13, sinks=8)
+    assert ops.max_pool_scores(q.cuda(), k.cuda(), 0.088).shape == (1, 1, 313, 313)
+    sel = [0, 150, 312]
+    for causal in (False, True):
+        ours = ops.max_pool_scores(q.cuda(), k.cuda(), 0.088, causal=causal).cpu()
+        ref = torch_ref.max_pool_map(q, k, 0.088, causal=causal, query_blocks=sel)
+        _max_pool_close(ours[:, :, sel], ref, what=f"causal={causal}")
 
 
 def test_attn_with_pooling_api_and_gqa():
@@ -133,7 +161,7 @@ def test_attn_with_pooling_api_and_gqa():
     o, po = attn_with_pooling(q.cuda(), k.cuda(), k.cuda(), False, 0.088, 128)
     assert o.shape == q.shape and not o.any()
     ref = torch_ref.max_pool_map(q, k, 0.088)
-    assert ((po.cpu().float() - ref.float()).abs() <= ref.float().abs() * 2 ** -7 + 1e-30).all()
+    _max_pool_close(po, ref)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

@@ -27,7 +27,7 @@ def lib():
 def test_header_declares_expected_entry_points():
     names = _declared()
     for n in ("sinkattn_block_sparse_plan", "sinkattn_block_sparse_fwd", "sinkattn_block_mass_pool",
-              "sinkattn_max_pool", "sinkattn_mean_pool_scores", "sinkattn_coverage_mask",
+              "sinkattn_max_pool", "sinkattn_max_pool_workspace_bytes", "sinkattn_mean_pool_scores", "sinkattn_coverage_mask",
               "sinkattn_last_error", "sinkattn_abi_version"):
         assert n in names
 
@@ -87,8 +87,8 @@ def test_pool_and_mask_validation(lib):
     s = _i64x4(0, 0, 128, 1)
     assert lib.sinkattn_block_mass_pool(16, 16, 0, 1, 1, 128, 128, 128, s, s, 64, 1.0, 16, 16, None) < 0
     assert "block_size" in _err(lib)
-    assert lib.sinkattn_max_pool(16, 16, 2, 1, 1, 1, 128, 128, s, s, 128, 1.0, 0, 16, None) < 0
-    assert lib.sinkattn_max_pool(16, 16, 0, 1, 4, 3, 128, 128, s, s, 128, 1.0, 0, 16, None) < 0
+    assert lib.sinkattn_max_pool(16, 16, 2, 1, 1, 1, 128, 128, s, s, 128, 1.0, 0, 16, 16, None) < 0
+    assert lib.sinkattn_max_pool(16, 16, 0, 1, 4, 3, 128, 128, s, s, 128, 1.0, 0, 16, 16, None) < 0
     assert "multiple" in _err(lib)
     assert lib.sinkattn_coverage_mask(16, 1, 1, 2000, 0.85, 1, 0, 0, 0, 0, 16, None, None, 16, None) < 0
     assert "1024" in _err(lib)

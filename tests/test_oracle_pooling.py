@@ -72,6 +72,21 @@ def test_max_pool_restatement_vs_formula():
     c = torch_ref.max_pool_map(qb, kb, sm, causal=True).float()
     assert torch.equal(c[0, 0, 0], torch.tensor([1.0, 0, 0, 0]))
     assert (torch.triu(c[0, 0], diagonal=1) == 0).all()
+    # causal against the definition with keys after the row removed: the reference's
+    # additive -1e6 on the diagonal tile drops them from every block maximum here
+    sc = s.masked_fill(torch.ones(512, 512, dtype=torch.bool).triu(1), float("-inf"))
+    bmc = sc.view(1, 2, 512, 4, 128).amax(-1)
+    ec = torch.exp2(bmc - bmc.amax(-1, keepdim=True)).view(1, 2, 4, 128, 4).amax(3)
+    assert torch.allclose(c.double(), ec / ec.sum(-1, keepdim=True), rtol=0.25, atol=1e-3)
+
+
+def test_max_pool_query_block_subset_matches_full_map():
+    q, k = _qk(1, 2, 700, 700, 128, seed=14)
+    qb, kb = q.bfloat16(), k.bfloat16()
+    for causal in (False, True):
+        full = torch_ref.max_pool_map(qb, kb, 0.09, causal=causal)
+        sub = torch_ref.max_pool_map(qb, kb, 0.09, causal=causal, query_blocks=[5, 0, 3])
+        assert torch.equal(sub, full[:, :, [5, 0, 3]])
 
 
 def test_mean_pool_closed_form():
