@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_kernel(FwdArgs a) {
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
-    mx = fmaxf(mx, xor32(mx));
+    mx = max_xor32(mx);
     const float m_new = fmaxf(m_run, mx * c);
     const float alpha = fast_exp2(m_run - m_new);
     l_run *= alpha;
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_kernel(FwdArgs a) {
     }
   }
 
-  const float l = l_run + xor32(l_run);
+  const float l = sum_xor32(l_run);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   if (qrow < a.Nq) {
     char* obase = (char*)a.out +
@@ -168,6 +168,8 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_kernel(FwdArgs a) {
 // physical chunk = logical ^ (row & 15) for K and logical ^ (4 * (row & 3)) for V, which
 // keeps the 16-lane K reads and the 32-lane transpose reads on distinct banks.
 // ------------------------------------------------------------------------------------
+constexpr float kLazyRescaleLog2 = 8.0f;
+
 template <int CT>
 __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a) {
   constexpr int DS = 8, DT = 4;
@@ -313,14 +315,18 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
-    mx = fmaxf(mx, xor32(mx));
-    const float m_new = fmaxf(m_run, __builtin_fmaf(mx, c, bias));
-    if (m_new != m_run) {
-      const float alpha = fast_exp2(m_run - m_new);
+    mx = max_xor32(mx);
+    // Lazy rescale: the reference point m_run moves only when this tile's maximum exceeds
+    // it by more than kLazyRescaleLog2, so P = exp2(c*s + bias - m_run) stays at most 2^8
+    // (well inside the range of bf16/f16 P and fp32 O, l) and the 64 multiplies of O run
+    // on few tiles.  O / l and m_run + log2(l) do not depend on the reference point.
+    const float m_tile = __builtin_fmaf(mx, c, bias);
+    if (m_tile > m_run + kLazyRescaleLog2) {
+      const float alpha = fast_exp2(m_run - m_tile);
       l_run *= alpha;
 #pragma unroll
       for (int i = 0; i < DT; ++i) o[i] *= alpha;
-      m_run = m_new;
+      m_run = m_tile;
     }
     // P in the MFMA's 16-bit type; the row sum adds those rounded values (one dot2 per
     // pair, four independent partial sums), so O and l are normalised by the same weights.
@@ -382,7 +388,7 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
     if (next) issue_v(it + 1);
   }
 
-  const float l = l_run + xor32(l_run);
+  const float l = sum_xor32(l_run);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   if (qrow < a.Nq) {
     char* obase = (char*)a.out + ((int64_t)b * a.os[0] + (int64_t)h * a.os[1] + (int64_t)qrow * a.os[2]) * 2;
@@ -523,7 +529,7 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_f32_kernel(FwdArgs a) {
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
-    mx = fmaxf(mx, xor32(mx));
+    mx = max_xor32(mx);
     const float m_new = fmaxf(m_run, mx * c);
     const float alpha = fast_exp2(m_run - m_new);
     l_run *= alpha;
@@ -564,7 +570,7 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_f32_kernel(FwdArgs a) {
     }
   }
 
-  const float l = l_run + xor32(l_run);
+  const float l = sum_xor32(l_run);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   if (qrow < a.Nq) {
     float* obase = (float*)a.out + ((int64_t)b * a.os[0] + (int64_t)h * a.os[1] + (int64_t)qrow * a.os[2]);

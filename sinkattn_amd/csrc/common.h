@@ -76,9 +76,21 @@ __device__ __forceinline__ f32x16 mfma32x32x16<kF16>(u32x4 a, u32x4 b, f32x16 c)
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// Cross-lane exchange with lane ^ 32 (the two halves of a 32x32 MFMA column).
-__device__ __forceinline__ float xor32(float x) {
-  return __shfl_xor(x, 32, 64);
+// Reductions over lane pairs (l, l ^ 32), the two halves of a 32x32 MFMA column, with one
+// v_permlane32_swap (a VALU op, no LDS round trip).  The swap of x with itself leaves
+// (x[l], x[l + 32]) in lane l < 32 and (x[l - 32], x[l]) in lane l >= 32, so both lanes of a
+// pair combine the same two values in the same order.
+__device__ __forceinline__ f32x2 pair32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return f32x2{__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const f32x2 p = pair32(x);
+  return fmaxf(p[0], p[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const f32x2 p = pair32(x);
+  return p[0] + p[1];
 }
 
 // Load 8 consecutive elements of type IT at p (16-byte aligned for 16-bit types,

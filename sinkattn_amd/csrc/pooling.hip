@@ -103,14 +103,14 @@ __global__ __launch_bounds__(256, 3) void block_mass_persistent_kernel(PoolArgs 
         for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
-        m_ref = fmaxf(mx, xor32(mx)) * c;
+        m_ref = max_xor32(mx) * c;
       }
       float ps = 0.f;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int j = 0; j < 16; ++j) ps += fast_exp2(__builtin_fmaf(s[t][j], c, -m_ref));
-      ps += xor32(ps);
+      ps = sum_xor32(ps);
       if (!(ps <= kSumLimit)) {
         // Rare: scores far above m_ref.  Move m_ref to this tile's maximum and rescale
         // the row's earlier sums (the two lanes of the row split them by parity).
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256, 3) void block_mass_persistent_kernel(PoolArgs 
         for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
-        mx = fmaxf(mx, xor32(mx)) * c;
+        mx = max_xor32(mx) * c;
         const float f = fast_exp2(m_ref - mx);
         for (int j = hl; j < kb; j += 2) ws[j * 128 + r] *= f;
         l_tot *= f;
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256, 3) void block_mass_persistent_kernel(PoolArgs 
         for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int j = 0; j < 16; ++j) ps += fast_exp2(__builtin_fmaf(s[t][j], c, -m_ref));
-        ps += xor32(ps);
+        ps = sum_xor32(ps);
       }
       l_tot += ps;
       if (hl == 0) ws[kb * 128 + r] = ps;
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(256) void block_mass_f32_kernel(PoolArgs a) {
       float mx = neg_inf();
 #pragma unroll
       for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[j]);
-      mx = fmaxf(mx, xor32(mx)) * c;
+      mx = max_xor32(mx) * c;
       if (mx > m_ref + kRescaleMargin) {
         const float f = fast_exp2(m_ref - mx);
         for (int j = hl; j < kb; j += 2) my[j] *= f;
@@ -236,14 +236,14 @@ __global__ __launch_bounds__(256) void block_mass_f32_kernel(PoolArgs a) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) ps += fast_exp2(__builtin_fmaf(s[j], c, -m_ref));
     }
-    ps += xor32(ps);
+    ps = sum_xor32(ps);
     if (hl == 0) my[kb] = ps;
   }
   __syncthreads();
   {
     float tot = 0.f;
     for (int j = hl; j < nkb; j += 2) tot += my[j];
-    tot += xor32(tot);
+    tot = sum_xor32(tot);
     if (hl == 0) row_tot[r] = tot;
   }
   __syncthreads();
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(256, 3) void max_pool_persistent_kernel(PoolArgs a,
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
-      mx = fmaxf(mx, xor32(mx)) * qk_scale;
+      mx = max_xor32(mx) * qk_scale;
       m = fmaxf(m, mx);
       if (hl == 0) ws[kb * 128 + r] = round_to<CT>(mx);
     }
