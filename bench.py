@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # 0.5 GiB for it -> x2.0, WRITE_SIZE reads 1 GiB -> x1.0).  Summaries with the commands:
 # profiles/block_sparse_fwd_wan_c2.md and profiles/block_mass_pool_wan_c2.md.
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
-TRAFFIC_KIB = {"fa": (1449874.0, 200750.0), "pool": (1283615.0, 792576.0)}
+TRAFFIC_KIB = {"fa": (1484972.0, 201386.0), "pool": (1277918.0, 792577.0)}
 
 
 def traffic_bytes(kind):
@@ -54,7 +54,7 @@ def _parse():
     p.add_argument("--no-extras", action="store_true", help="skip dense/pooling/mask timings")
     p.add_argument("--cpu-sample-qblocks", type=int, default=0,
                    help="q-blocks of the layer the CPU baseline times (0 = the whole layer, 6144)")
-    p.add_argument("--only", choices=["all", "fa", "pool", "mask"], default="all",
+    p.add_argument("--only", choices=["all", "fa", "pool", "maxpool", "mask"], default="all",
                    help="profiling aid: run just one kernel family (no JSON line unless 'all')")
     p.add_argument("--copy-mb", type=int, default=0,
                    help="profiling aid: first run a device copy of this many MiB (counter calibration)")
@@ -203,6 +203,7 @@ def main():
 
     if args.only != "all":
         fn = {"fa": step, "pool": lambda: ops.block_mass_scores(q, k),
+              "maxpool": lambda: ops.max_pool_scores(q, k, 1.0 / math.sqrt(D)),
               "mask": lambda: ops.coverage_mask(torch.rand(H, 256, 256, device=dev), 0.85, True)}[args.only]
         for _ in range(args.warmup + args.steps):
             fn()
