@@ -252,6 +252,19 @@ def main():
         out["dense_same_kernel_ms"] = round(dms, 3)
         out["dense_same_kernel_tflops"] = round(dense_flops / (dms * 1e-3) / 1e12, 2)
         out["sparse_over_dense_time"] = round(ms / dms, 4)
+        # torch's own dense attention on ROCm (the reference's dense path), restricted to the
+        # flash backend so that no bf16 batched-GEMM fallback runs
+        try:
+            import torch.nn.functional as F
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+            qc, kc, vc = (x.contiguous() for x in (q, k, v))
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                sms = time_fn(torch, lambda: F.scaled_dot_product_attention(qc, kc, vc), 3, 1)
+            out["dense_torch_sdpa_flash_ms"] = round(sms, 3)
+            out["dense_torch_sdpa_flash_tflops"] = round(dense_flops / (sms * 1e-3) / 1e12, 2)
+            del qc, kc, vc
+        except Exception as ex:  # backend not built into this torch
+            out["dense_torch_sdpa_flash_ms"] = f"unavailable: {type(ex).__name__}"
         pms = time_fn(torch, lambda: ops.block_mass_scores(q, k), 3, 1)
         pool_flops = 2.0 * B * H * N * N * D
         pool_bytes = 2 * q.numel() * 2 + B * H * 256 * 256 * 4
