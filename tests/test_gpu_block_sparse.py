@@ -76,6 +76,30 @@ def test_small_random_masks(dtype, N):
     _check(out, lse, q, k, v, mask)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("step", [7.5, 30.0, -12.0])
+def test_running_maximum_moves_across_tiles(dtype, step):
+    # Key block j gets a score offset of j * step log2 units (through channel 0: q = 1,
+    # k = offset / (scale * log2 e)), so the row maximum rises slowly (the softmax reference
+    # point lags it by up to 8 and P reaches ~2^7.5), rises fast (moves on every tile) or
+    # falls (never moves after the first tile).
+    B, H, N, D = 1, 2, 1024, 128
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(B, H, N, D, generator=g) * 0.5
+    k = torch.randn(B, H, N, D, generator=g) * 0.5
+    v = torch.randn(B, H, N, D, generator=g)
+    c = (1.0 / math.sqrt(D)) * 1.4426950408889634
+    q[..., 0] = 1.0
+    offs = torch.arange(N) // 128 * step
+    offs = offs - offs.min()
+    k[..., 0] = (offs / c).round()
+    q, k, v = (x.to("cuda", dtype) for x in (q, k, v))
+    mask = _random_mask(B, H, 8, 8, 0.7, seed=5)
+    out, lse = ops.block_sparse_attention(q, k, v, ops.block_sparse_plan(mask))
+    torch.cuda.synchronize()
+    _check(out, lse, q, k, v, mask)
+
+
 def test_config1_shape_fp32_with_sinks():
     # B=1, H=12, N=4096, d=128, fp32, 4 sink keys scaled 8x.
     q, k, v = _inputs(1, 12, 4096, 4096, 128, torch.float32, seed=0, sink_keys=4)
