@@ -390,19 +390,36 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
 
   const float l = sum_xor32(l_run);
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  if (qrow < a.Nq) {
-    char* obase = (char*)a.out + ((int64_t)b * a.os[0] + (int64_t)h * a.os[1] + (int64_t)qrow * a.os[2]) * 2;
+  // O goes out through this wave's 8 KB of the (now idle) K buffer: each lane holds 4-value
+  // pieces of its own row, so direct stores would be 32 partial rows per instruction; after
+  // the transpose every store instruction writes 4 whole 256-byte rows.  Every wave has
+  // passed the last barrier (no wave still reads K, no copy into it is in flight), and
+  // each wave touches only its own slice.
+  {
+    SA_LDS char* ob = lk + wave * 8192;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int d = dt * 32 + 8 * g + 4 * hl;
-        store4<CT>(obase + d * 2, o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
-                   o[dt][4 * g + 3] * inv);
+        const int chunk = (dt * 4 + g) ^ (l32 & 15);
+        u32x2 w;
+        w[0] = pack2<CT>(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv);
+        w[1] = pack2<CT>(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+        *(SA_LDS u32x2*)(ob + l32 * 256 + chunk * 16 + hl * 8) = w;
       }
-    if (a.lse != nullptr && hl == 0)
-      a.lse[((int64_t)b * a.H + h) * a.Nq + qrow] = ntot > 0 ? (m_run + __log2f(l)) * kLn2 : pos_inf();
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0) only
+    const int q0 = qb * 128 + wave * 32;
+    char* obase = (char*)a.out + ((int64_t)b * a.os[0] + (int64_t)h * a.os[1]) * 2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = 4 * i + (lane >> 4), c = lane & 15;
+      const u32x4 val = *(SA_LDS const u32x4*)(ob + rr * 256 + ((c ^ (rr & 15)) * 16));
+      if (q0 + rr < a.Nq)
+        *reinterpret_cast<u32x4*>(obase + ((int64_t)(q0 + rr) * a.os[2]) * 2 + c * 16) = val;
+    }
   }
+  if (qrow < a.Nq && a.lse != nullptr && hl == 0)
+    a.lse[((int64_t)b * a.H + h) * a.Nq + qrow] = ntot > 0 ? (m_run + __log2f(l)) * kLn2 : pos_inf();
 }
 
 // fp32 operands: every value is split as x = hi + lo with hi = bf16(x) and
