@@ -108,6 +108,7 @@ hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream);
 hipError_t launch_block_sparse_fwd(const FwdArgs& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);
 int block_mass_groups();
+int device_cu_count();
 hipError_t launch_max_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_mean_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_coverage_mask(const MaskArgs& a, hipStream_t stream);

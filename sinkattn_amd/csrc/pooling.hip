@@ -448,15 +448,18 @@ __global__ __launch_bounds__(64) void mean_pool_scores_kernel(PoolArgs a, int D)
 }
 
 // ------------------------------------------------------------------------------------
-// Resident work-groups of the persistent block-mass kernel on the current device.
-int block_mass_groups() {
+// Compute units of the current device (256, an MI355X, if the query fails).
+int device_cu_count() {
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
   }
-  return 3 * cus;
+  return cus;
 }
+
+// Resident work-groups of the persistent block-mass kernel on the current device.
+int block_mass_groups() { return 3 * device_cu_count(); }
 
 hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream) {
   (void)D;
