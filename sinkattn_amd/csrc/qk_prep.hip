@@ -18,7 +18,9 @@
 
 namespace sa {
 
-template <int IT, int CPL, int GS>
+// SHARED: GS is a multiple of a head's chunk count, so all chunks of a lane sit at the
+// same offset within their heads and need the same table entries (loaded once per row).
+template <int IT, int CPL, int GS, bool SHARED>
 __global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepArgs a, int64_t row_step) {
   constexpr int ES = ElemSize<IT>::value;
   constexpr int EPC = 16 / ES;  // elements per 16-byte chunk (8 for 16-bit types)
@@ -66,7 +68,7 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepArgs a, int64_t row_
       if (live && c < chunks) {
         const int col = c * EPC;
         xv[i] = *reinterpret_cast<const u32x4*>(src + c * 16);
-        if (rot) {
+        if (rot && (i == 0 || !SHARED)) {
           const int p0 = (col % a.D) / 2;  // first pair of this chunk within its head
           if constexpr (EPC == 8) {
             rv[i][0] = *reinterpret_cast<const f32x4*>(fre + p0);
@@ -113,7 +115,8 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepArgs a, int64_t row_
           if constexpr (IT == kBF16) { y0 = (float)(__bf16)y0; y1 = (float)(__bf16)y1; }
           if constexpr (IT == kF16) { y0 = (float)(_Float16)y0; y1 = (float)(_Float16)y1; }
           if (rot) {
-            const float re = rv[i][0][pr], im = iv[i][0][pr];
+            const int ti = SHARED ? 0 : i;
+            const float re = rv[ti][0][pr], im = iv[ti][0][pr];
             o[2 * pr] = y0 * re - y1 * im;
             o[2 * pr + 1] = y0 * im + y1 * re;
           } else {
@@ -138,11 +141,17 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepArgs a, int64_t row_
 // grid.y = 0 for Q, 1 for K; grid.x work-groups of four waves, at most eight per CU.
 template <int IT, int CPL, int GS>
 static hipError_t launch_qk_prep_g(const QkPrepArgs& a, hipStream_t stream) {
+  constexpr int EPC = IT == kF32 ? 4 : 8;
   constexpr int RPW = 64 / GS;
   const int64_t need = (a.rows + 4 * RPW - 1) / (4 * RPW);
   const int64_t cap = (int64_t)8 * device_cu_count();
   const int gx = (int)(need < cap ? need : cap);
-  qk_prep_kernel<IT, CPL, GS><<<dim3((unsigned)gx, 2), 256, 0, stream>>>(a, (int64_t)gx * 4 * RPW);
+  const dim3 grid((unsigned)gx, 2);
+  const int64_t step = (int64_t)gx * 4 * RPW;
+  if (GS % (a.D / EPC) == 0)
+    qk_prep_kernel<IT, CPL, GS, true><<<grid, 256, 0, stream>>>(a, step);
+  else
+    qk_prep_kernel<IT, CPL, GS, false><<<grid, 256, 0, stream>>>(a, step);
   return hipGetLastError();
 }
 
