@@ -629,11 +629,14 @@ __global__ __launch_bounds__(256) void plan_rows_kernel(PlanArgs a) {
 // which q-blocks share an XCD's L2 (4 MB).  The q-blocks of one head read the same K/V,
 // so the resident work-groups of an XCD (32 CUs x 2) should come from one head at a
 // time.  Each head is cut into chunks of about kChunkQb q-blocks (qb = j mod C, C =
-// chunks per head); chunks are dealt to the 8 XCDs longest-processing-time first (cost
-// = listed tiles + one per q-block), at most ceil(chunks / 8) per XCD, so every XCD
-// gets the same number of chunks and nearly the same work whatever the per-head
-// densities; an XCD runs its chunks in (head, j) order and a chunk's q-blocks longest
-// first.  Slots past the end of a shorter chunk hold -1.
+// chunks per head).  When the chunk count is not a multiple of 8, the heads of the last,
+// partial round are cut finer (C * F chunks each, F = 8 / gcd(their chunks, 8)), so that
+// every XCD can get the same share of them.  Whole chunks, then the fine chunks, are dealt
+// to the 8 XCDs longest-processing-time first (cost = listed tiles + one per q-block), each
+// kind at most ceil(count / 8) per XCD, so every XCD gets nearly the same work whatever the
+// per-head densities; an XCD runs its whole chunks, then its fine chunks, each kind in
+// (head, j) order, and a chunk's q-blocks longest first.  Slots past the end of a shorter
+// chunk hold -1.
 constexpr int kChunkQb = 128;
 constexpr int kMaxChunks = 4096;
 
@@ -642,58 +645,115 @@ __host__ __device__ inline int chunks_per_head(int nqb) {
   return c < 1 ? 1 : c;
 }
 
+// Chunk layout of a plan: heads [0, nbh_w) in Cw chunks of at most Sw q-blocks, heads
+// [nbh_w, nbh) in Cs = Cw * F chunks of at most Ss q-blocks.
+struct ChunkLayout {
+  int nbh, nbh_w, Cw, Sw, Cs, Ss, nw, ns, cap_w, cap_s;
+  __host__ __device__ int slots_per_xcd() const { return cap_w * Sw + cap_s * Ss; }
+};
+
+__host__ __device__ inline int gcd_int(int x, int y) {
+  while (y != 0) {
+    const int t = x % y;
+    x = y;
+    y = t;
+  }
+  return x;
+}
+
+__host__ __device__ inline ChunkLayout chunk_layout(int nbh, int nqb) {
+  ChunkLayout L;
+  L.nbh = nbh;
+  L.Cw = chunks_per_head(nqb);
+  L.Sw = (nqb + L.Cw - 1) / L.Cw;
+  const int rem = (nbh * L.Cw) % kXcds;  // chunks of the partial last round
+  const int nsplit = rem == 0 ? 0 : (rem + L.Cw - 1) / L.Cw;
+  L.nbh_w = nbh - nsplit;
+  int F = kXcds / gcd_int(nsplit * L.Cw, kXcds);
+  while (F > 1 && L.Cw * F > nqb) F >>= 1;  // a fine chunk keeps at least one q-block
+  L.Cs = L.Cw * F;
+  L.Ss = (nqb + L.Cs - 1) / L.Cs;
+  L.nw = L.nbh_w * L.Cw;
+  L.ns = nsplit * L.Cs;
+  L.cap_w = (L.nw + kXcds - 1) / kXcds;
+  L.cap_s = (L.ns + kXcds - 1) / kXcds;
+  return L;
+}
+
 __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
   __shared__ int cost[kMaxChunks];
   __shared__ int16_t sorted[kMaxChunks];
   __shared__ uint8_t xcd[kMaxChunks];
   __shared__ int16_t pos[kMaxChunks];
-  const int nbh = a.rows / a.nqb;
-  const int C = chunks_per_head(a.nqb);
-  const int S = (a.nqb + C - 1) / C;  // q-blocks per chunk (at most)
-  const int nch = nbh * C;
-  const int per_xcd = (nch + kXcds - 1) / kXcds;
-  const int total = per_xcd * S * kXcds;
+  const ChunkLayout L = chunk_layout(a.rows / a.nqb, a.nqb);
+  const int nch = L.nw + L.ns;
+  const int total = L.slots_per_xcd() * kXcds;
+  // chunk ch -> (head, residue j, modulus)
+  auto chunk_head = [&](int ch, int& bh, int& j, int& C) {
+    if (ch < L.nw) {
+      bh = ch / L.Cw;
+      j = ch - bh * L.Cw;
+      C = L.Cw;
+    } else {
+      const int f = ch - L.nw;
+      bh = L.nbh_w + f / L.Cs;
+      j = f % L.Cs;
+      C = L.Cs;
+    }
+  };
   for (int i = threadIdx.x; i < total; i += blockDim.x) a.order[i] = -1;
   for (int ch = threadIdx.x; ch < nch; ch += blockDim.x) {
-    const int bh = ch / C, j = ch - bh * C;
+    int bh, j, C;
+    chunk_head(ch, bh, j, C);
     int w = 0;
     for (int qb = j; qb < a.nqb; qb += C) w += a.counts[bh * a.nqb + qb] + 1;
     cost[ch] = w;
   }
   __syncthreads();
-  for (int ch = threadIdx.x; ch < nch; ch += blockDim.x) {  // rank by cost desc, index asc
+  // rank by cost desc, index asc, within each kind (whole chunks, then fine chunks)
+  for (int ch = threadIdx.x; ch < nch; ch += blockDim.x) {
+    const int lo = ch < L.nw ? 0 : L.nw, hi = ch < L.nw ? L.nw : nch;
     const int w = cost[ch];
-    int r = 0;
-    for (int c2 = 0; c2 < nch; ++c2) r += (cost[c2] > w) || (cost[c2] == w && c2 < ch);
+    int r = lo;
+    for (int c2 = lo; c2 < hi; ++c2) r += (cost[c2] > w) || (cost[c2] == w && c2 < ch);
     sorted[r] = (int16_t)ch;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     int load[kXcds], n[kXcds];
-    for (int x = 0; x < kXcds; ++x) load[x] = n[x] = 0;
-    for (int r = 0; r < nch; ++r) {
-      const int ch = sorted[r];
-      int best = -1;
-      for (int x = 0; x < kXcds; ++x)
-        if (n[x] < per_xcd && (best < 0 || load[x] < load[best])) best = x;
-      xcd[ch] = (uint8_t)best;
-      load[best] += cost[ch];
-      ++n[best];
+    for (int x = 0; x < kXcds; ++x) load[x] = 0;
+    for (int kind = 0; kind < 2; ++kind) {
+      const int lo = kind == 0 ? 0 : L.nw, hi = kind == 0 ? L.nw : nch;
+      const int cap = kind == 0 ? L.cap_w : L.cap_s;
+      for (int x = 0; x < kXcds; ++x) n[x] = 0;
+      for (int r = lo; r < hi; ++r) {
+        const int ch = sorted[r];
+        int best = -1;
+        for (int x = 0; x < kXcds; ++x)
+          if (n[x] < cap && (best < 0 || load[x] < load[best])) best = x;
+        xcd[ch] = (uint8_t)best;
+        load[best] += cost[ch];
+        ++n[best];
+      }
+      for (int x = 0; x < kXcds; ++x) n[x] = 0;
+      for (int ch = lo; ch < hi; ++ch) pos[ch] = (int16_t)(n[xcd[ch]]++);
     }
-    for (int x = 0; x < kXcds; ++x) n[x] = 0;
-    for (int ch = 0; ch < nch; ++ch) pos[ch] = (int16_t)(n[xcd[ch]]++);
   }
   __syncthreads();
   for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
     const int bh = row / a.nqb, qb = row - bh * a.nqb;
-    const int j = qb % C, ch = bh * C + j;
+    const bool fine = bh >= L.nbh_w;
+    const int C = fine ? L.Cs : L.Cw;
+    const int j = qb % C;
+    const int ch = fine ? L.nw + (bh - L.nbh_w) * L.Cs + j : bh * L.Cw + j;
     const int c = a.counts[row];
     int rank = 0;
     for (int q2 = j; q2 < a.nqb; q2 += C) {
       const int c2 = a.counts[bh * a.nqb + q2];
       rank += (c2 > c) || (c2 == c && q2 < qb);
     }
-    a.order[(pos[ch] * S + rank) * kXcds + xcd[ch]] = row;
+    const int slot = fine ? L.cap_w * L.Sw + pos[ch] * L.Ss + rank : pos[ch] * L.Sw + rank;
+    a.order[slot * kXcds + xcd[ch]] = row;
   }
 }
 
@@ -717,14 +777,16 @@ __global__ __launch_bounds__(256) void plan_order_interleaved_kernel(PlanArgs a)
   }
 }
 
-static bool chunked_order(int rows, int nqb) { return rows / nqb * chunks_per_head(nqb) <= kMaxChunks; }
+static bool chunked_order(int rows, int nqb) {
+  const ChunkLayout L = chunk_layout(rows / nqb, nqb);
+  return L.nw + L.ns <= kMaxChunks;
+}
 
 int plan_order_slots(int rows, int nqb) {
   if (rows == 0 || nqb == 0) return 0;
   const int nbh = rows / nqb;
   if (!chunked_order(rows, nqb)) return nbh * ((nqb + kXcds - 1) / kXcds) * kXcds;
-  const int C = chunks_per_head(nqb);
-  return (nbh * C + kXcds - 1) / kXcds * ((nqb + C - 1) / C) * kXcds;
+  return chunk_layout(nbh, nqb).slots_per_xcd() * kXcds;
 }
 
 hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream) {

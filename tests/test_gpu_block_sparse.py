@@ -149,26 +149,47 @@ def test_head_dim_64_and_cross_lengths():
     _check(out, lse[..., 0], q, k, v, mask)
 
 
+def _chunk_layout(nbh, nqb):
+    """Chunking of the launch order: heads [0, nbh_w) in Cw chunks (qb mod Cw), the heads
+    of the partial last round of 8 in Cs = Cw * F finer chunks."""
+    from math import gcd
+    Cw = max(1, nqb // 128)
+    rem = (nbh * Cw) % 8
+    nsplit = 0 if rem == 0 else -(-rem // Cw)
+    F = 8 // gcd(nsplit * Cw, 8)
+    while F > 1 and Cw * F > nqb:
+        F //= 2
+    Cs = Cw * F
+    nbh_w = nbh - nsplit
+    return dict(nbh_w=nbh_w, Cw=Cw, Sw=-(-nqb // Cw), Cs=Cs, Ss=-(-nqb // Cs),
+                nw=nbh_w * Cw, ns=nsplit * Cs)
+
+
 def _check_order(plan, counts, nbh, nqb):
-    """Launch-order invariants: a permutation of the rows; slot i runs on XCD i % 8;
-    a head is cut into C = max(1, nqb // 128) chunks (qb mod C), each chunk on one XCD,
-    at most ceil(chunks / 8) chunks per XCD, run in (head, chunk) order, each chunk's
-    q-blocks longest first; LPT keeps the XCD loads within one chunk's cost."""
+    """Launch-order invariants: a permutation of the rows; slot i runs on XCD i % 8; every
+    chunk (q-blocks qb = j mod C of one head) on one XCD; per XCD at most ceil(n / 8) chunks
+    of each kind (whole, then fine), each kind in (head, j) order in consecutive slot
+    blocks, each chunk's q-blocks longest first; LPT keeps the XCD loads within one chunk's
+    cost."""
+    L = _chunk_layout(nbh, nqb)
+    cap_w, cap_s = -(-L["nw"] // 8), -(-L["ns"] // 8)
     order = plan.order.cpu().tolist()
     rows = nbh * nqb
     real = sorted(r for r in order if r >= 0)
     assert real == list(range(rows))
-    C = max(1, nqb // 128)
-    S = -(-nqb // C)
-    nch = nbh * C
-    per_xcd = -(-nch // 8)
-    assert len(order) == per_xcd * S * 8
+    assert len(order) == (cap_w * L["Sw"] + cap_s * L["Ss"]) * 8
+
+    def chunk_of(r):
+        bh, qb = divmod(r, nqb)
+        if bh < L["nbh_w"]:
+            return bh * L["Cw"] + qb % L["Cw"]
+        return L["nw"] + (bh - L["nbh_w"]) * L["Cs"] + qb % L["Cs"]
+
     chunk_xcd, seq = {}, {x: [] for x in range(8)}
     for i, r in enumerate(order):
         if r < 0:
             continue
-        bh, qb = divmod(r, nqb)
-        ch = bh * C + qb % C
+        ch = chunk_of(r)
         assert chunk_xcd.setdefault(ch, i % 8) == i % 8
         seq[i % 8].append((i // 8, ch, int(counts[r])))
     load = [0] * 8
@@ -178,22 +199,31 @@ def _check_order(plan, counts, nbh, nqb):
             if not chs or chs[-1] != ch:
                 chs.append(ch)
             load[x] += c + 1
-        assert chs == sorted(chs) and len(chs) <= per_xcd
-        for ch in chs:  # a chunk's q-blocks in slots pos*S .. pos*S + S-1, longest first
+        assert chs == sorted(chs)
+        whole = [ch for ch in chs if ch < L["nw"]]
+        fine = [ch for ch in chs if ch >= L["nw"]]
+        assert len(whole) <= cap_w and len(fine) <= cap_s
+        for ch in chs:  # a chunk's q-blocks in its slot block, longest first
             ks = [k for k, c2, _ in seq[x] if c2 == ch]
             cs = [c for _, c2, c in seq[x] if c2 == ch]
-            pos = chs.index(ch)
-            assert all(pos * S <= k < (pos + 1) * S for k in ks)
+            if ch < L["nw"]:
+                lo = whole.index(ch) * L["Sw"]
+                hi = lo + L["Sw"]
+            else:
+                lo = cap_w * L["Sw"] + fine.index(ch) * L["Ss"]
+                hi = lo + L["Ss"]
+            assert all(lo <= k < hi for k in ks)
             assert cs == sorted(cs, reverse=True)
-    chunk_cost = [0] * nch
+    chunk_cost = {}
     for r in range(rows):
-        bh, qb = divmod(r, nqb)
-        chunk_cost[bh * C + qb % C] += int(counts[r]) + 1
+        chunk_cost[chunk_of(r)] = chunk_cost.get(chunk_of(r), 0) + int(counts[r]) + 1
+    nch = L["nw"] + L["ns"]
     busy = [l for l in load if l > 0]
-    assert max(busy) - min(load if nch >= 8 else busy) <= max(chunk_cost)
+    assert max(busy) - min(load if nch >= 8 else busy) <= max(chunk_cost.values())
 
 
-@pytest.mark.parametrize("B,H,nqb,nkb,density", [(2, 3, 7, 9, 0.35), (1, 5, 300, 40, 0.3), (2, 12, 256, 256, 0.2)])
+@pytest.mark.parametrize("B,H,nqb,nkb,density", [(2, 3, 7, 9, 0.35), (1, 5, 300, 40, 0.3), (2, 12, 256, 256, 0.2),
+                                                 (1, 30, 132, 132, 0.15), (1, 3, 2, 2, 0.5)])
 def test_plan_lists_and_order(B, H, nqb, nkb, density):
     mask = _random_mask(B, H, nqb, nkb, density, seed=12, diag=False, col0=False, empty_rows=1)
     plan = ops.block_sparse_plan(mask)
