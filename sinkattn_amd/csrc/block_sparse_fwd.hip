@@ -639,6 +639,7 @@ __global__ __launch_bounds__(256) void plan_rows_kernel(PlanArgs a) {
 // chunk hold -1.
 constexpr int kChunkQb = 128;
 constexpr int kMaxChunks = 4096;
+constexpr int kMaxOutliers = 1024;
 
 __host__ __device__ inline int chunks_per_head(int nqb) {
   const int c = nqb / kChunkQb;
@@ -682,7 +683,7 @@ __host__ __device__ inline ChunkLayout chunk_layout(int nbh, int nqb) {
 
 __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
   __shared__ int cost[kMaxChunks];
-  __shared__ int16_t sorted[kMaxChunks];
+  __shared__ int16_t sorted[kMaxChunks + 2 * kXcds];  // later also 8 * (cap_s + cap_w)
   __shared__ uint8_t xcd[kMaxChunks];
   __shared__ int16_t pos[kMaxChunks];
   const ChunkLayout L = chunk_layout(a.rows / a.nqb, a.nqb);
@@ -740,20 +741,97 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
     }
   }
   __syncthreads();
-  for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
+  // Sequence of each XCD: its outliers first (q-blocks costing more than twice the XCD's
+  // mean, longest first: a long row started late ends the launch late), then its fine
+  // chunks, then its whole chunks (each kind by position), each chunk's other q-blocks
+  // longest first.  Outliers are fewer than half of an XCD's q-blocks; past kMaxOutliers
+  // in the whole plan none are taken out (the chunk sequence alone).
+  __shared__ int xsum[kXcds], xcnt[kXcds], nout[kXcds], nlist;
+  __shared__ int outl[kMaxOutliers];
+  __shared__ int16_t nonout[kMaxChunks];
+  int* chunk_off = cost;   // the chunk costs are spent once the XCDs are assigned
+  int16_t* seq = sorted;   // so is the ranking: it becomes each XCD's chunk sequence
+  if (threadIdx.x < kXcds) xsum[threadIdx.x] = xcnt[threadIdx.x] = nout[threadIdx.x] = 0;
+  if (threadIdx.x == 0) nlist = 0;
+  // seq[x * (cap_s + cap_w) + k]: the k-th chunk of XCD x (fine chunks, then whole)
+  const int per_x = L.cap_s + L.cap_w;
+  for (int i = threadIdx.x; i < per_x * kXcds; i += blockDim.x) seq[i] = -1;
+  __syncthreads();
+  for (int ch = threadIdx.x; ch < nch; ch += blockDim.x)
+    seq[xcd[ch] * per_x + (ch < L.nw ? L.cap_s : 0) + pos[ch]] = (int16_t)ch;
+  auto chunk_of = [&](int row, int& C, int& j) {
     const int bh = row / a.nqb, qb = row - bh * a.nqb;
     const bool fine = bh >= L.nbh_w;
-    const int C = fine ? L.Cs : L.Cw;
-    const int j = qb % C;
-    const int ch = fine ? L.nw + (bh - L.nbh_w) * L.Cs + j : bh * L.Cw + j;
-    const int c = a.counts[row];
-    int rank = 0;
-    for (int q2 = j; q2 < a.nqb; q2 += C) {
-      const int c2 = a.counts[bh * a.nqb + q2];
-      rank += (c2 > c) || (c2 == c && q2 < qb);
+    C = fine ? L.Cs : L.Cw;
+    j = qb % C;
+    return fine ? L.nw + (bh - L.nbh_w) * L.Cs + j : bh * L.Cw + j;
+  };
+  for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
+    int C, j;
+    const int x = xcd[chunk_of(row, C, j)];
+    atomicAdd(&xsum[x], a.counts[row] + 1);
+    atomicAdd(&xcnt[x], 1);
+  }
+  __syncthreads();
+  auto above = [&](int row, int x) {
+    return (int64_t)(a.counts[row] + 1) * xcnt[x] > 2 * (int64_t)xsum[x];
+  };
+  for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
+    int C, j;
+    const int x = xcd[chunk_of(row, C, j)];
+    if (above(row, x)) {
+      atomicAdd(&nout[x], 1);
+      const int k = atomicAdd(&nlist, 1);
+      if (k < kMaxOutliers) outl[k] = row;
     }
-    const int slot = fine ? L.cap_w * L.Sw + pos[ch] * L.Ss + rank : pos[ch] * L.Sw + rank;
-    a.order[slot * kXcds + xcd[ch]] = row;
+  }
+  __syncthreads();
+  const bool use_out = nlist <= kMaxOutliers;
+  for (int ch = threadIdx.x; ch < nch; ch += blockDim.x) {  // non-outlier count per chunk
+    int bh, j, C;
+    chunk_head(ch, bh, j, C);
+    int n = 0;
+    for (int qb = j; qb < a.nqb; qb += C) n += !(use_out && above(bh * a.nqb + qb, xcd[ch]));
+    nonout[ch] = (int16_t)n;
+  }
+  __syncthreads();
+  if (threadIdx.x < kXcds) {  // offsets along each XCD's chunk sequence
+    const int x = threadIdx.x;
+    int off = use_out ? nout[x] : 0;
+    for (int k = 0; k < per_x; ++k) {
+      const int ch = seq[x * per_x + k];
+      if (ch < 0) continue;
+      chunk_off[ch] = off;
+      off += nonout[ch];
+    }
+  }
+  __syncthreads();
+  for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
+    int C, j;
+    const int ch = chunk_of(row, C, j);
+    const int x = xcd[ch];
+    const int bh = row / a.nqb, qb = row - bh * a.nqb;
+    const int c = a.counts[row];
+    int slot = 0;
+    if (use_out && above(row, x)) {
+      for (int k = 0; k < nlist; ++k) {
+        const int r2 = outl[k];
+        int C2, j2;
+        if (r2 == row || xcd[chunk_of(r2, C2, j2)] != x) continue;
+        const int c2 = a.counts[r2];
+        slot += (c2 > c) || (c2 == c && r2 < row);
+      }
+    } else {
+      int rank = 0;
+      for (int q2 = j; q2 < a.nqb; q2 += C) {
+        const int r2 = bh * a.nqb + q2;
+        if (use_out && above(r2, x)) continue;
+        const int c2 = a.counts[r2];
+        rank += (c2 > c) || (c2 == c && q2 < qb);
+      }
+      slot = chunk_off[ch] + rank;
+    }
+    a.order[slot * kXcds + x] = row;
   }
 }
 

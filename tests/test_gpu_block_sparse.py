@@ -165,12 +165,17 @@ def _chunk_layout(nbh, nqb):
                 nw=nbh_w * Cw, ns=nsplit * Cs)
 
 
+MAX_OUTLIERS = 1024  # q-blocks taken out of the chunk sequences, in the whole plan
+
+
 def _check_order(plan, counts, nbh, nqb):
     """Launch-order invariants: a permutation of the rows; slot i runs on XCD i % 8; every
-    chunk (q-blocks qb = j mod C of one head) on one XCD; per XCD at most ceil(n / 8) chunks
-    of each kind (whole, then fine), each kind in (head, j) order in consecutive slot
-    blocks, each chunk's q-blocks longest first; LPT keeps the XCD loads within one chunk's
-    cost."""
+    chunk (q-blocks qb = j mod C of one head) on one XCD, at most ceil(n / 8) chunks of each
+    kind (whole, fine) per XCD; each XCD's slots hold, from slot 0: its outliers (cost =
+    tiles + 1 above twice the XCD's mean; none when the plan has more than MAX_OUTLIERS) by
+    cost desc, then its fine chunks, then its whole chunks (each kind in ascending chunk
+    order), each chunk's other q-blocks by cost desc; LPT keeps the XCD loads within one
+    chunk's cost."""
     L = _chunk_layout(nbh, nqb)
     cap_w, cap_s = -(-L["nw"] // 8), -(-L["ns"] // 8)
     order = plan.order.cpu().tolist()
@@ -185,38 +190,37 @@ def _check_order(plan, counts, nbh, nqb):
             return bh * L["Cw"] + qb % L["Cw"]
         return L["nw"] + (bh - L["nbh_w"]) * L["Cs"] + qb % L["Cs"]
 
-    chunk_xcd, seq = {}, {x: [] for x in range(8)}
+    cost = [int(counts[r]) + 1 for r in range(rows)]
+    chunk_xcd = {}
     for i, r in enumerate(order):
-        if r < 0:
-            continue
-        ch = chunk_of(r)
-        assert chunk_xcd.setdefault(ch, i % 8) == i % 8
-        seq[i % 8].append((i // 8, ch, int(counts[r])))
+        if r >= 0:
+            assert chunk_xcd.setdefault(chunk_of(r), i % 8) == i % 8
+    mine_of = [[r for r in range(rows) if chunk_xcd[chunk_of(r)] == x] for x in range(8)]
+    sums = [sum(cost[r] for r in m) for m in mine_of]
+    outliers = [[r for r in m if cost[r] * len(m) > 2 * sums[x]] for x, m in enumerate(mine_of)]
+    if sum(len(o) for o in outliers) > MAX_OUTLIERS:
+        outliers = [[] for _ in range(8)]
     load = [0] * 8
     for x in range(8):
-        chs = []
-        for k, ch, c in seq[x]:
-            if not chs or chs[-1] != ch:
-                chs.append(ch)
-            load[x] += c + 1
-        assert chs == sorted(chs)
-        whole = [ch for ch in chs if ch < L["nw"]]
-        fine = [ch for ch in chs if ch >= L["nw"]]
-        assert len(whole) <= cap_w and len(fine) <= cap_s
-        for ch in chs:  # a chunk's q-blocks in its slot block, longest first
-            ks = [k for k, c2, _ in seq[x] if c2 == ch]
-            cs = [c for _, c2, c in seq[x] if c2 == ch]
-            if ch < L["nw"]:
-                lo = whole.index(ch) * L["Sw"]
-                hi = lo + L["Sw"]
-            else:
-                lo = cap_w * L["Sw"] + fine.index(ch) * L["Ss"]
-                hi = lo + L["Ss"]
-            assert all(lo <= k < hi for k in ks)
-            assert cs == sorted(cs, reverse=True)
+        mine = mine_of[x]
+        load[x] = sums[x]
+        chs = sorted({chunk_of(r) for r in mine})
+        assert len([c for c in chs if c < L["nw"]]) <= cap_w
+        assert len([c for c in chs if c >= L["nw"]]) <= cap_s
+        if not mine:
+            assert all(order[k * 8 + x] == -1 for k in range(len(order) // 8))
+            continue
+        out = set(outliers[x])
+        want = sorted(out, key=lambda r: (-cost[r], r))
+        for ch in [c for c in chs if c >= L["nw"]] + [c for c in chs if c < L["nw"]]:
+            rest = [r for r in mine if chunk_of(r) == ch and r not in out]
+            want += sorted(rest, key=lambda r: (-cost[r], r))
+        got = [order[k * 8 + x] for k in range(len(order) // 8)]
+        assert got[: len(want)] == want
+        assert all(r == -1 for r in got[len(want):])
     chunk_cost = {}
     for r in range(rows):
-        chunk_cost[chunk_of(r)] = chunk_cost.get(chunk_of(r), 0) + int(counts[r]) + 1
+        chunk_cost[chunk_of(r)] = chunk_cost.get(chunk_of(r), 0) + cost[r]
     nch = L["nw"] + L["ns"]
     busy = [l for l in load if l > 0]
     assert max(busy) - min(load if nch >= 8 else busy) <= max(chunk_cost.values())
@@ -235,6 +239,19 @@ def test_plan_lists_and_order(B, H, nqb, nkb, density):
         assert counts[r].item() == want.numel()
         assert torch.equal(idx[r, : want.numel()], want)
     _check_order(plan, counts, B * H, nqb)
+
+
+@pytest.mark.parametrize("B,H,nqb,full,density", [(1, 30, 132, 0.03, 0.15), (2, 12, 256, 0.1, 0.05),
+                                                  (2, 12, 256, 0.4, 0.0), (1, 5, 300, 0.02, 0.1)])
+def test_plan_order_long_rows_first(B, H, nqb, full, density):
+    # Masks with a share of fully dense q-block rows (the text rows of Z-Image's joint
+    # sequence, the prefix rows of the coverage mask): those rows lead their XCD's sequence,
+    # unless the plan holds more than MAX_OUTLIERS of them (the 40% case).
+    g = torch.Generator().manual_seed(50)
+    m = torch.rand(B, H, nqb, nqb, generator=g) < density
+    m[torch.rand(B, H, nqb, generator=g) < full] = True
+    plan = ops.block_sparse_plan(m.cuda())
+    _check_order(plan, plan.counts.cpu(), B * H, nqb)
 
 
 def test_bad_mask_shape_raises():
