@@ -392,7 +392,9 @@ int sinkattn_block_mass_pool(const void* q, const void* k, int dtype, int64_t B,
 
 size_t sinkattn_max_pool_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t block_size, int dtype) {
   if (dtype == SINKATTN_F32 || block_size <= 0) return 0;
-  return sinkattn_block_mass_pool_workspace_bytes(B, H, N, N, block_size, dtype);
+  const int64_t items = B * H * cdiv(N, block_size);
+  const int64_t groups = items < sa::max_pool_groups() ? items : sa::max_pool_groups();
+  return (size_t)(groups * cdiv(N, block_size) * 128 * (int64_t)sizeof(float));
 }
 
 int sinkattn_max_pool(const void* q, const void* k, int dtype, int64_t B, int64_t H, int64_t Hk,

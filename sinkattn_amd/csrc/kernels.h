@@ -109,6 +109,9 @@ hipError_t launch_block_sparse_fwd(const FwdArgs& a, int dtype, int D, hipStream
 hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);
 int block_mass_groups();
 int device_cu_count();
+// Resident work-groups of the persistent max-pool kernel: its workspace holds one slot per
+// group, so the launch and the workspace query both use this count.
+int max_pool_groups();
 hipError_t launch_max_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_mean_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_coverage_mask(const MaskArgs& a, hipStream_t stream);

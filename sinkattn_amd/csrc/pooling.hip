@@ -270,9 +270,10 @@ __device__ __forceinline__ float round_to<kF16>(float x) {
 
 // ------------------------------------------------------------------------------------
 // Max-pool map, persistent form (bf16/f16): the structure of block_mass_persistent_kernel
-// (3 groups per CU, K tiles by DMA, S^T on the matrix cores) with the block maxima of each
-// row kept in the group's workspace slot ws[kb][row] instead of LDS, so three groups fit
-// a CU.  Per tile: R[r,kb] = q.dtype(max_j s * sm_scale * log2e) (raw-score maximum first,
+// (K tiles by DMA, S^T on the matrix cores) with the block maxima of each row kept in the
+// group's workspace slot ws[kb][row] instead of LDS, so four groups (37 KB of LDS, 128
+// VGPRs each) fit a CU: per tile a group waits for its own copy, and the other three
+// cover that wait.  Per tile: R[r,kb] = q.dtype(max_j s * sm_scale * log2e) (raw-score maximum first,
 // then the scale, as pooling_kernel.py:39-48 does), m_r = max over kb of the unrounded
 // values.  Epilogue per kb: Po[kb] = q.dtype(max over the block's rows of
 // exp2(R[r,kb] - m_r)), then the row is normalised in q.dtype (pooling_kernel.py:65-75,
@@ -280,7 +281,7 @@ __device__ __forceinline__ float round_to<kF16>(float x) {
 // diagonal of the diagonal tile.
 // ------------------------------------------------------------------------------------
 template <int CT>
-__global__ __launch_bounds__(256, 3) void max_pool_persistent_kernel(PoolArgs a, int items) {
+__global__ __launch_bounds__(256, 4) void max_pool_persistent_kernel(PoolArgs a, int items) {
   constexpr int DS = 8;
   __shared__ u32x4 lds_k[2048];
   __shared__ float row_m[128];
@@ -295,9 +296,8 @@ __global__ __launch_bounds__(256, 3) void max_pool_persistent_kernel(PoolArgs a,
   const int drow = 4 * wave + (lane >> 4);
   const uint32_t k_off = (uint32_t)drow * kstride + (uint32_t)(((lane & 15) ^ (drow & 15)) * 16);
   const int prow = k_row_perm(l32);
-  uint32_t ka[DS];
-#pragma unroll
-  for (int ds = 0; ds < DS; ++ds) ka[ds] = (uint32_t)(prow * 256 + (((2 * ds + hl) ^ (prow & 15)) * 16));
+  // chunk (2ds + hl) ^ (prow & 15) of row prow: the k-step only flips bits 5-7
+  const uint32_t ka0 = (uint32_t)(prow * 256 + ((hl ^ (prow & 15)) * 16));
   SA_LDS char* lk = (SA_LDS char*)lds_k;
   // The reference forms qk_scale = fp32(sm_scale) * fp32(1.44269504).
   const float qk_scale = a.scale * 1.44269504f;
@@ -330,13 +330,27 @@ __global__ __launch_bounds__(256, 3) void max_pool_persistent_kernel(PoolArgs a,
       f32x16 s[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) s[t] = f32x16{};
+      {
+        // Flat step i = 4 ds + t.  The read for step i + 2 is issued right after the MFMA
+        // of step i (the scheduling groups pin that order), so each read has two MFMAs to
+        // land; a deeper ring does not fit the 128 VGPRs of four groups per CU.
+        u32x4 kr[4];
+        auto kread = [&](int i) __attribute__((always_inline)) {
+          return *(SA_LDS const u32x4*)(lk + (ka0 ^ (32u * (i >> 2))) + (i & 3) * 8192);
+        };
+        kr[0] = kread(0);
+        kr[1] = kread(1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const u32x4 av = *(SA_LDS const u32x4*)(lk + ka[ds] + t * 8192);
-          s[t] = mfma32x32x16<CT>(av, qf[ds], s[t]);
+        for (int i = 0; i < 4 * DS; ++i) {
+          s[i & 3] = mfma32x32x16<CT>(kr[i & 3], qf[i >> 2], s[i & 3]);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (i + 2 < 4 * DS) {
+            kr[(i + 2) & 3] = kread(i + 2);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
         }
+      }
       const bool diag = a.causal && kb == qb;
       if (key0 + 128 > a.Nk || diag) {
 #pragma unroll
@@ -460,6 +474,7 @@ int device_cu_count() {
 
 // Resident work-groups of the persistent block-mass kernel on the current device.
 int block_mass_groups() { return 3 * device_cu_count(); }
+int max_pool_groups() { return 4 * device_cu_count(); }
 
 hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream) {
   (void)D;
@@ -483,7 +498,7 @@ hipError_t launch_max_pool(const PoolArgs& a, int dtype, int D, hipStream_t stre
   (void)D;
   if (a.B * a.H * a.nqb == 0) return hipSuccess;
   const int items = a.B * a.H * a.nqb;
-  const int groups = min(items, block_mass_groups());
+  const int groups = min(items, max_pool_groups());
   if (dtype == kBF16)
     max_pool_persistent_kernel<kBF16><<<groups, 256, 0, stream>>>(a, items);
   else
