@@ -640,6 +640,7 @@ __global__ __launch_bounds__(256) void plan_rows_kernel(PlanArgs a) {
 constexpr int kChunkQb = 128;
 constexpr int kMaxChunks = 4096;
 constexpr int kMaxOutliers = 1024;
+constexpr int kPlanLdsRows = 16384;
 
 __host__ __device__ inline int chunks_per_head(int nqb) {
   const int c = nqb / kChunkQb;
@@ -681,14 +682,39 @@ __host__ __device__ inline ChunkLayout chunk_layout(int nbh, int nqb) {
   return L;
 }
 
+template <bool STAGED>
 __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
   __shared__ int cost[kMaxChunks];
   __shared__ int16_t sorted[kMaxChunks + 2 * kXcds];  // later also 8 * (cap_s + cap_w)
   __shared__ uint8_t xcd[kMaxChunks];
   __shared__ int16_t pos[kMaxChunks];
+  // The passes below read each q-block's tile count many times.  STAGED (rows <=
+  // kPlanLdsRows): they are copied to LDS once (eight coalesced loads in flight per
+  // thread) and read there; otherwise they are read from global memory.
+  __shared__ int cnt_lds[STAGED ? kPlanLdsRows : 1];
   const ChunkLayout L = chunk_layout(a.rows / a.nqb, a.nqb);
   const int nch = L.nw + L.ns;
   const int total = L.slots_per_xcd() * kXcds;
+  if constexpr (STAGED) {
+    for (int base = 0; base < a.rows; base += 8 * 256) {
+      int v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = base + u * 256 + (int)threadIdx.x;
+        v[u] = i < a.rows ? a.counts[i] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = base + u * 256 + (int)threadIdx.x;
+        if (i < a.rows) cnt_lds[i] = v[u];
+      }
+    }
+    __syncthreads();
+  }
+  auto counts = [&](int row) __attribute__((always_inline)) {
+    if constexpr (STAGED) return cnt_lds[row];
+    else return a.counts[row];
+  };
   // chunk ch -> (head, residue j, modulus)
   auto chunk_head = [&](int ch, int& bh, int& j, int& C) {
     if (ch < L.nw) {
@@ -707,7 +733,7 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
     int bh, j, C;
     chunk_head(ch, bh, j, C);
     int w = 0;
-    for (int qb = j; qb < a.nqb; qb += C) w += a.counts[bh * a.nqb + qb] + 1;
+    for (int qb = j; qb < a.nqb; qb += C) w += counts(bh * a.nqb + qb) + 1;
     cost[ch] = w;
   }
   __syncthreads();
@@ -747,7 +773,9 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
   // longest first.  Outliers are fewer than half of an XCD's q-blocks; past kMaxOutliers
   // in the whole plan none are taken out (the chunk sequence alone).
   __shared__ int xsum[kXcds], xcnt[kXcds], nout[kXcds], nlist;
-  __shared__ int outl[kMaxOutliers];
+  __shared__ int outl[kMaxOutliers], outl_c[kMaxOutliers];
+  __shared__ uint8_t outl_x[kMaxOutliers];
+  __shared__ int wave_keys[4][256];
   __shared__ int16_t nonout[kMaxChunks];
   int* chunk_off = cost;   // the chunk costs are spent once the XCDs are assigned
   int16_t* seq = sorted;   // so is the ranking: it becomes each XCD's chunk sequence
@@ -769,17 +797,18 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
   for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
     int C, j;
     const int x = xcd[chunk_of(row, C, j)];
-    atomicAdd(&xsum[x], a.counts[row] + 1);
+    atomicAdd(&xsum[x], counts(row) + 1);
     atomicAdd(&xcnt[x], 1);
   }
   __syncthreads();
-  auto above = [&](int row, int x) {
-    return (int64_t)(a.counts[row] + 1) * xcnt[x] > 2 * (int64_t)xsum[x];
+  // a q-block of `c` tiles on XCD x is an outlier when (c + 1) * count > 2 * sum
+  auto above = [&](int c, int x) __attribute__((always_inline)) {
+    return (int64_t)(c + 1) * xcnt[x] > 2 * (int64_t)xsum[x];
   };
   for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
     int C, j;
     const int x = xcd[chunk_of(row, C, j)];
-    if (above(row, x)) {
+    if (above(counts(row), x)) {
       atomicAdd(&nout[x], 1);
       const int k = atomicAdd(&nlist, 1);
       if (k < kMaxOutliers) outl[k] = row;
@@ -787,11 +816,21 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
   }
   __syncthreads();
   const bool use_out = nlist <= kMaxOutliers;
+  if (use_out) {  // XCD and tile count of every listed outlier
+    for (int k = threadIdx.x; k < nlist; k += blockDim.x) {
+      const int r = outl[k];
+      int C, j;
+      outl_x[k] = xcd[chunk_of(r, C, j)];
+      outl_c[k] = counts(r);
+    }
+  }
   for (int ch = threadIdx.x; ch < nch; ch += blockDim.x) {  // non-outlier count per chunk
     int bh, j, C;
     chunk_head(ch, bh, j, C);
+    const int64_t xc = xcnt[xcd[ch]], xs2 = 2 * (int64_t)xsum[xcd[ch]];
     int n = 0;
-    for (int qb = j; qb < a.nqb; qb += C) n += !(use_out && above(bh * a.nqb + qb, xcd[ch]));
+    for (int qb = j; qb < a.nqb; qb += C)
+      n += !(use_out && (int64_t)(counts(bh * a.nqb + qb) + 1) * xc > xs2);
     nonout[ch] = (int16_t)n;
   }
   __syncthreads();
@@ -806,32 +845,63 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
     }
   }
   __syncthreads();
-  for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
-    int C, j;
-    const int ch = chunk_of(row, C, j);
-    const int x = xcd[ch];
-    const int bh = row / a.nqb, qb = row - bh * a.nqb;
-    const int c = a.counts[row];
-    int slot = 0;
-    if (use_out && above(row, x)) {
-      for (int k = 0; k < nlist; ++k) {
-        const int r2 = outl[k];
-        int C2, j2;
-        if (r2 == row || xcd[chunk_of(r2, C2, j2)] != x) continue;
-        const int c2 = a.counts[r2];
-        slot += (c2 > c) || (c2 == c && r2 < row);
+  // Outliers: rank among the XCD's outliers by cost desc, then row asc.
+  if (use_out) {
+    for (int k = threadIdx.x; k < nlist; k += blockDim.x) {
+      const int r = outl[k], x = outl_x[k], c = outl_c[k];
+      int slot = 0;
+      for (int k2 = 0; k2 < nlist; ++k2) {
+        const int c2 = outl_c[k2];
+        slot += (k2 != k) & (outl_x[k2] == x) & ((c2 > c) | ((c2 == c) & (outl[k2] < r)));
       }
-    } else {
-      int rank = 0;
-      for (int q2 = j; q2 < a.nqb; q2 += C) {
-        const int r2 = bh * a.nqb + q2;
-        if (use_out && above(r2, x)) continue;
-        const int c2 = a.counts[r2];
-        rank += (c2 > c) || (c2 == c && q2 < qb);
-      }
-      slot = chunk_off[ch] + rank;
+      a.order[slot * kXcds + x] = r;
     }
-    a.order[slot * kXcds + x] = row;
+  }
+  // The other q-blocks: one wave per chunk.  A chunk has at most 255 q-blocks (chunks
+  // split heads of >= 128 q-blocks into pieces of 128-255), four per lane.  Their keys go
+  // to the wave's LDS row in q order: count * 256 + (255 - k) for the k-th q-block of the
+  // chunk (more tiles first, then lower q), -1 for an outlier and past the chunk's end.
+  // Every lane ranks its four against the row, 16 bytes per broadcast read, with one
+  // comparison per pair and no branches.
+  {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int* keys = wave_keys[wv];
+    for (int ch = wv; ch < nch; ch += 4) {
+      int bh, j, C;
+      chunk_head(ch, bh, j, C);
+      const int S = (a.nqb - j + C - 1) / C;
+      const int x = xcd[ch];
+      const int64_t xc = use_out ? xcnt[x] : 0, xs2 = 2 * (int64_t)xsum[x];
+      int key[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int k = lane + 64 * u;
+        key[u] = -1;
+        if (k < S) {
+          const int c = counts(bh * a.nqb + j + k * C);
+          if ((int64_t)(c + 1) * xc <= xs2) key[u] = c * 256 + (255 - k);
+        }
+        keys[k] = key[u];
+      }
+      // the wave's LDS writes land before its reads (in order within a wave)
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_wave_barrier();
+      int rank[4] = {0, 0, 0, 0};
+      for (int k2 = 0; k2 < S; k2 += 4) {
+        const i32x4 v = *reinterpret_cast<const i32x4*>(keys + k2);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) rank[u] += v[e] > key[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int k = lane + 64 * u;
+        if (key[u] >= 0) a.order[(chunk_off[ch] + rank[u]) * kXcds + x] = bh * a.nqb + j + k * C;
+      }
+      // every lane has read the row before the next chunk overwrites it
+      __builtin_amdgcn_wave_barrier();
+    }
   }
 }
 
@@ -872,8 +942,10 @@ hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream) {
   plan_rows_kernel<<<(a.rows + 3) / 4, 256, 0, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.order == nullptr) return e;
-  if (chunked_order(a.rows, a.nqb))
-    plan_order_kernel<<<1, 256, 0, stream>>>(a);
+  if (chunked_order(a.rows, a.nqb) && a.rows <= kPlanLdsRows)
+    plan_order_kernel<true><<<1, 256, 0, stream>>>(a);
+  else if (chunked_order(a.rows, a.nqb))
+    plan_order_kernel<false><<<1, 256, 0, stream>>>(a);
   else
     plan_order_interleaved_kernel<<<1, 256, 0, stream>>>(a);
   return hipGetLastError();

@@ -227,7 +227,8 @@ def _check_order(plan, counts, nbh, nqb):
 
 
 @pytest.mark.parametrize("B,H,nqb,nkb,density", [(2, 3, 7, 9, 0.35), (1, 5, 300, 40, 0.3), (2, 12, 256, 256, 0.2),
-                                                 (1, 30, 132, 132, 0.15), (1, 3, 2, 2, 0.5)])
+                                                 (1, 30, 132, 132, 0.15), (1, 3, 2, 2, 0.5),
+                                                 (2, 40, 210, 64, 0.2)])
 def test_plan_lists_and_order(B, H, nqb, nkb, density):
     mask = _random_mask(B, H, nqb, nkb, density, seed=12, diag=False, col0=False, empty_rows=1)
     plan = ops.block_sparse_plan(mask)
@@ -242,11 +243,13 @@ def test_plan_lists_and_order(B, H, nqb, nkb, density):
 
 
 @pytest.mark.parametrize("B,H,nqb,full,density", [(1, 30, 132, 0.03, 0.15), (2, 12, 256, 0.1, 0.05),
-                                                  (2, 12, 256, 0.4, 0.0), (1, 5, 300, 0.02, 0.1)])
+                                                  (2, 12, 256, 0.4, 0.0), (1, 5, 300, 0.02, 0.1),
+                                                  (2, 40, 210, 0.02, 0.1)])
 def test_plan_order_long_rows_first(B, H, nqb, full, density):
     # Masks with a share of fully dense q-block rows (the text rows of Z-Image's joint
     # sequence, the prefix rows of the coverage mask): those rows lead their XCD's sequence,
-    # unless the plan holds more than MAX_OUTLIERS of them (the 40% case).
+    # unless the plan holds more than MAX_OUTLIERS of them (the 40% case).  The last case
+    # has more q-blocks (16800) than the ordering kernel stages in LDS.
     g = torch.Generator().manual_seed(50)
     m = torch.rand(B, H, nqb, nqb, generator=g) < density
     m[torch.rand(B, H, nqb, generator=g) < full] = True
