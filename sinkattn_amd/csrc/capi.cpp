@@ -152,6 +152,8 @@ int block_sparse_fwd_impl(const void* q, const void* k, const void* v, int dtype
     if ((rc = check_operand("vd", comp.vd, comp.vds)) != 0) return rc;
     if (comp.kds[2] != k_strides[2] || comp.vds[2] != v_strides[2])
       return fail("fwd_comp: kd/vd row strides must equal k/v row strides");
+    if (comp.Nd * k_strides[2] * 2 >= (int64_t)1 << 31 || comp.Nd * v_strides[2] * 2 >= (int64_t)1 << 31)
+      return fail("fwd_comp: one head of kd or vd spans more than 2 GiB");
     if (!(comp.log_gap >= 0.f) || comp.log_gap > 64.f) return fail("fwd_comp: log_gap %g out of range", comp.log_gap);
     a.kd = comp.kd;
     a.vd = comp.vd;

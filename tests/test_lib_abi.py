@@ -105,3 +105,15 @@ def test_workspace_queries(lib):
     assert lib.sinkattn_block_mass_pool_workspace_bytes(1, 12, 4096, 4096, 128, 2) == 0
     assert lib.sinkattn_block_mass_pool_workspace_bytes(2, 12, 32760, 32760, 128, 0) % (256 * 512) == 0
     assert lib.sinkattn_abi_version() >= 1
+
+
+def test_fwd_rejects_heads_past_the_32bit_copy_range(lib):
+    # K/V tiles are copied through buffer descriptors with a 32-bit byte range: one head of
+    # k/v (and of the compensation kd/vd) must stay under 2 GiB.
+    nk = 1 << 20
+    sq, sk = _i64x4(0, 0, 128, 1), _i64x4(0, 0, 1536, 1)
+    args = [16, 16, 16, 0, 1, 1, 128, nk, 128, sq, sk, sk, 16, sq, None, 16, 16, None, 1, nk // 128, 1.0, None]
+    assert lib.sinkattn_block_sparse_fwd(*args) < 0 and "2 GiB" in _err(lib)
+    comp = [16, 16, 16, 0, 1, 1, 128, 128, 128, sq, sk, sk, 16, 16, sk, sk, nk, 1, 1.0,
+            16, sq, None, 16, 16, None, 1, 1, 1.0, None]
+    assert lib.sinkattn_block_sparse_fwd_comp(*comp) < 0 and "kd or vd" in _err(lib)
