@@ -173,11 +173,14 @@ int sinkattn_lse_mix(const void* sink_out, const int64_t sink_strides[4],
  *     P = softmax_rows(scale * Q K^T)                  (fp32, over all Nk keys)
  *     out[b,h,qb,kb] = mean over the rows r of q-block qb of  sum_{j in kb} P[r,j]
  * out is fp32 [B,H,nqb,nkb] contiguous, nqb = ceil(Nq/block), nkb = ceil(Nk/block).
- * bf16/f16 inputs use the bf16/f16 matrix cores (products are exact, sums fp32) and a
- * device workspace of sinkattn_block_mass_pool_workspace_bytes() bytes (per-row block
- * sums of the resident work-groups, queried for the current device); f32 inputs use the
- * fp32 matrix cores and need no workspace (pass NULL).  block_size must be 128 and
- * nkb <= 256 for f32.
+ * block_size 128 with D 128: bf16/f16 inputs use the bf16/f16 matrix cores (products are
+ * exact, sums fp32) and a device workspace of sinkattn_block_mass_pool_workspace_bytes()
+ * bytes (per-row block sums of the resident work-groups, queried for the current
+ * device); f32 inputs use the fp32 matrix cores (nkb <= 256) and need no workspace.
+ * Every other shape (block_size 1..1024, D 1..256, f32 with nkb > 256) runs a generic
+ * kernel (fp32 dot products, two passes over the keys, no workspace; the query may still
+ * return a size for block_size 128, which the call then leaves unused), limited by LDS to
+ * about (160 KiB / 4 - 128 (D + 1) - 4160) key blocks.
  * ---------------------------------------------------------------------------------- */
 size_t sinkattn_block_mass_pool_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nk,
                                                 int64_t block_size, int dtype);
@@ -196,13 +199,16 @@ int sinkattn_block_mass_pool(const void* q, const void* k, int dtype,
  *     m_r      = max over kb of the unrounded block maxima
  *     Po[qb,kb]= q.dtype( max_{r in qb} exp2(R[r,kb] - m_r) )
  *     Po      /= q.dtype( sum_kb Po[qb,kb] )           (row normalisation in q.dtype)
- * Po is written in q.dtype (bf16 or f16) as [B,H,nd,nd] contiguous.  kv head of query
+ Po is written in q.dtype (bf16, f16 or f32) as [B,H,nd,nd] contiguous.  kv head of query
  * head h is h / (H / Hk).  causal restricts row qb to kb <= qb and adds -1e6 to the
  * raw scores above the diagonal of the diagonal tile, as the reference does.  Keys and
- * rows >= N are excluded (the reference leaves ragged N undefined).  block_size = 128,
- * D = 128, nd <= 1024.  `workspace` is a device buffer of at least
- * sinkattn_max_pool_workspace_bytes(...) bytes (per-(row, key-block) maxima of the
- * rows in flight); calls that share one workspace must be ordered on one stream.
+ * rows >= N are excluded (the reference leaves ragged N undefined).  block_size in
+ * {16, 32, 64, 128}, D in {16, 32, 64, 128, 256} (the reference's asserts).  bf16/f16 with
+ * block_size 128, D 128 and nd <= 1024 run the persistent MFMA kernel: `workspace` is a
+ * device buffer of at least sinkattn_max_pool_workspace_bytes(...) bytes (per-(row,
+ * key-block) maxima of the rows in flight); calls that share one workspace must be
+ * ordered on one stream.  Other shapes run the generic kernel (no workspace; same LDS
+ * bound as the generic block-mass kernel).
  * ---------------------------------------------------------------------------------- */
 size_t sinkattn_max_pool_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t block_size,
                                          int dtype);
@@ -243,7 +249,7 @@ int sinkattn_mean_pool_scores(const void* q, const void* k, int dtype,
  * The reference's empty-row fallback is reproduced as written: if any row of the whole
  * tensor ends up empty, every row r gets mask[r, top1(r)] = (row r was empty), which
  * also clears that bit in non-empty rows.  workspace: *_workspace_bytes(H, nq).
- * nk <= 1024.
+ * nk <= 4096.
  * ---------------------------------------------------------------------------------- */
 size_t sinkattn_coverage_mask_workspace_bytes(int64_t H, int64_t nq);
 int sinkattn_coverage_mask(const float* scores, int64_t H, int64_t nq, int64_t nk,

@@ -23,6 +23,7 @@ ARCH = os.environ.get("SINKATTN_ARCH", "gfx950")
 SOURCES = [
     "block_sparse_fwd.hip",
     "pooling.hip",
+    "pooling_generic.hip",
     "coverage_mask.hip",
     "compensation.hip",
     "qk_prep.hip",

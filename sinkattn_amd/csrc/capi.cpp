@@ -334,8 +334,9 @@ static int fill_pool_args(sa::PoolArgs& a, const char* who, const void* q, const
                           int64_t B, int64_t H, int64_t Hk, int64_t Nq, int64_t Nk, int64_t D,
                           const int64_t* qs, const int64_t* ks, int64_t block_size) {
   if (!valid_dtype(dtype)) return fail("%s: unsupported dtype %d", who, dtype);
-  if (block_size != 128) return fail("%s: block_size %lld not supported (128)", who, (long long)block_size);
-  if (D != 128) return fail("%s: head dim %lld not supported (128)", who, (long long)D);
+  if (block_size < 1 || block_size > 1024)
+    return fail("%s: block_size %lld not supported (1..1024)", who, (long long)block_size);
+  if (D < 1 || D > 1024) return fail("%s: head dim %lld not supported", who, (long long)D);
   if (B < 0 || H < 0 || Hk <= 0 || Nq < 0 || Nk < 0) return fail("%s: bad size", who);
   if (H % Hk != 0) return fail("%s: query heads %lld not a multiple of kv heads %lld", who, (long long)H, (long long)Hk);
   if (Nq > kMaxInt || Nk > kMaxInt || B * H * cdiv(Nq, 128) > kMaxInt) return fail("%s: sizes exceed int32", who);
@@ -357,6 +358,17 @@ static int fill_pool_args(sa::PoolArgs& a, const char* who, const void* q, const
   a.Nk = (int)Nk;
   a.nqb = (int)cdiv(Nq, block_size);
   a.nkb = (int)cdiv(Nk, block_size);
+  a.bs = (int)block_size;
+  a.D = (int)D;
+  return 0;
+}
+
+// The generic pooling kernels (any block size and head dim) hold a query-row group, a key
+// tile, a score tile and one map row in LDS.
+static int check_generic_pool(const char* who, const sa::PoolArgs& a, int dtype) {
+  if (a.D > 256) return fail("%s: head dim %d above 256 needs block_size 128 and head dim 128", who, a.D);
+  if (sa::generic_pool_lds_need(a.D, a.nkb, dtype) > sa::kGenericPoolMaxLds)
+    return fail("%s: %d key blocks of head dim %d exceed the generic kernel's LDS", who, a.nkb, a.D);
   return 0;
 }
 
@@ -377,19 +389,22 @@ int sinkattn_block_mass_pool(const void* q, const void* k, int dtype, int64_t B,
                           k_strides, block_size);
   if (rc != 0) return rc;
   if (Nk == 0) return fail("block_mass_pool: no keys");
-  if (dtype == SINKATTN_F32 && a.nkb > 256)
-    return fail("block_mass_pool: %d key blocks exceed the supported 256 for f32", a.nkb);
   if (out == nullptr) return fail("block_mass_pool: null output");
-  if (dtype != SINKATTN_F32) {
+  a.scale = scale;
+  a.out = out;
+  a.ws = reinterpret_cast<float*>(workspace);
+  const bool at128 = block_size == 128 && D == 128;
+  if (at128 && dtype != SINKATTN_F32) {  // persistent MFMA kernel, workspace slots
     if (workspace == nullptr) return fail("block_mass_pool: null workspace");
     if (k_strides[2] < D) return fail("block_mass_pool: k row stride below the head dim");
     if (Nk * k_strides[2] * 2 >= (int64_t)1 << 31)
       return fail("block_mass_pool: one head of k spans more than 2 GiB");
+    return hip_status(sa::launch_block_mass_pool(a, dtype, (int)D, (hipStream_t)stream), "pool launch");
   }
-  a.scale = scale;
-  a.out = out;
-  a.ws = reinterpret_cast<float*>(workspace);
-  return hip_status(sa::launch_block_mass_pool(a, dtype, (int)D, (hipStream_t)stream), "pool launch");
+  if (at128 && a.nkb <= 256)  // fp32 MFMA kernel
+    return hip_status(sa::launch_block_mass_pool(a, dtype, (int)D, (hipStream_t)stream), "pool launch");
+  if ((rc = check_generic_pool("block_mass_pool", a, dtype)) != 0) return rc;
+  return hip_status(sa::launch_block_mass_generic(a, dtype, (hipStream_t)stream), "pool launch");
 }
 
 size_t sinkattn_max_pool_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t block_size, int dtype) {
@@ -404,21 +419,29 @@ int sinkattn_max_pool(const void* q, const void* k, int dtype, int64_t B, int64_
                       int64_t block_size, float sm_scale, int causal, void* po, void* workspace,
                       void* stream) {
   sa::PoolArgs a{};
-  if (dtype == SINKATTN_F32) return fail("max_pool: q.dtype must be bf16 or f16");
   int rc = fill_pool_args(a, "max_pool", q, k, dtype, B, H, Hk, N, N, D, q_strides, k_strides,
                           block_size);
   if (rc != 0) return rc;
-  if (a.nkb > 1024) return fail("max_pool: %d key blocks exceed the supported 1024", a.nkb);
+  // the reference's asserts (pooling_kernel.py:198-207)
+  if (block_size != 16 && block_size != 32 && block_size != 64 && block_size != 128)
+    return fail("max_pool: block_size %lld not in {16, 32, 64, 128}", (long long)block_size);
+  if (D != 16 && D != 32 && D != 64 && D != 128 && D != 256)
+    return fail("max_pool: head dim %lld not in {16, 32, 64, 128, 256}", (long long)D);
   if (B * H * N == 0) return 0;
   if (po == nullptr) return fail("max_pool: null output");
-  if (workspace == nullptr) return fail("max_pool: null workspace (see sinkattn_max_pool_workspace_bytes)");
-  if (k_strides[2] < D || N * k_strides[2] * 2 >= (int64_t)1 << 31)
-    return fail("max_pool: k row stride below the head dim or one head of k over 2 GiB");
   a.scale = sm_scale;
   a.causal = causal ? 1 : 0;
   a.out = po;
   a.ws = static_cast<float*>(workspace);
-  return hip_status(sa::launch_max_pool(a, dtype, (int)D, (hipStream_t)stream), "max_pool launch");
+  if (dtype != SINKATTN_F32 && block_size == 128 && D == 128 && a.nkb <= 1024) {
+    // persistent MFMA kernel, workspace slots
+    if (workspace == nullptr) return fail("max_pool: null workspace (see sinkattn_max_pool_workspace_bytes)");
+    if (k_strides[2] < D || N * k_strides[2] * 2 >= (int64_t)1 << 31)
+      return fail("max_pool: k row stride below the head dim or one head of k over 2 GiB");
+    return hip_status(sa::launch_max_pool(a, dtype, (int)D, (hipStream_t)stream), "max_pool launch");
+  }
+  if ((rc = check_generic_pool("max_pool", a, dtype)) != 0) return rc;
+  return hip_status(sa::launch_max_pool_generic(a, dtype, (hipStream_t)stream), "max_pool launch");
 }
 
 size_t sinkattn_mean_pool_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nk, int64_t D,
@@ -453,7 +476,7 @@ int sinkattn_coverage_mask(const float* scores, int64_t H, int64_t nq, int64_t n
                            int64_t text_blocks, uint8_t* mask, int32_t* counts, int32_t* idx,
                            void* workspace, void* stream) {
   if (H < 0 || nq < 0 || nk < 0) return fail("coverage_mask: negative size");
-  if (nk > 1024) return fail("coverage_mask: %lld key blocks exceed the supported 1024", (long long)nk);
+  if (nk > 4096) return fail("coverage_mask: %lld key blocks exceed the supported 4096", (long long)nk);
   if (H * nq > kMaxInt) return fail("coverage_mask: too many rows");
   if (mode != 0 && mode != 1) return fail("coverage_mask: mode must be 0 (joint) or 1 (video_residual)");
   if (req_q < 0 || req_k < 0 || text_blocks < 0) return fail("coverage_mask: negative block count");

@@ -29,7 +29,10 @@
 
 namespace sa {
 
-constexpr int kMaskMaxN = 1024;
+// Row capacities: rows of up to 1024 key blocks use the small instance (21 KB of LDS),
+// longer rows (up to 4096) the large one (84 KB, one work-group per CU).
+constexpr int kMaskSmallN = 1024;
+constexpr int kMaskMaxN = 4096;
 
 // --- ATen-compatible fp32 row sum ---------------------------------------------------
 // x[i] * mul(i) is summed; mul is 1 (plain) or the 0/1 required flag (masked sum).
@@ -301,12 +304,13 @@ __device__ __forceinline__ uint32_t order_key(float x) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+template <int NMAX>
 __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
-  __shared__ float row[kMaskMaxN];
-  __shared__ unsigned long long keys[kMaskMaxN];
-  __shared__ float sv[kMaskMaxN];    // sorted values (tie-exact order when needed)
-  __shared__ int si[kMaskMaxN];      // sorted indices
-  __shared__ uint8_t m[kMaskMaxN];
+  __shared__ float row[NMAX];
+  __shared__ unsigned long long keys[NMAX];
+  __shared__ float sv[NMAX];    // sorted values (tie-exact order when needed)
+  __shared__ int si[NMAX];      // sorted indices
+  __shared__ uint8_t m[NMAX];
   __shared__ float sums_sh[2];
   __shared__ int k_sh, exact_sh;
 
@@ -472,10 +476,11 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
 // 371-374) runs when ANY row of the tensor is empty and then sets mask[r, top1[r]] =
 // empty[r] for EVERY row r -- it also clears the top-1 bit of non-empty rows.  Then the
 // ascending index lists and counts of the final mask are written.
+template <int NMAX>
 __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
-  __shared__ float sv[kMaskMaxN];
-  __shared__ int si[kMaskMaxN];
-  __shared__ uint8_t m[kMaskMaxN];
+  __shared__ float sv[NMAX];
+  __shared__ int si[NMAX];
+  __shared__ uint8_t m[NMAX];
   const int lane = threadIdx.x;
   const int rid = blockIdx.x;
   const int rows = a.H * a.nq;
@@ -524,10 +529,18 @@ __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
 hipError_t launch_coverage_mask(const MaskArgs& a, hipStream_t stream) {
   const int rows = a.H * a.nq;
   if (rows == 0 || a.nk == 0) return hipSuccess;
-  coverage_mask_kernel<<<rows, 64, 0, stream>>>(a);
+  if (a.nk <= kMaskSmallN) {
+    coverage_mask_kernel<kMaskSmallN><<<rows, 64, 0, stream>>>(a);
+  } else {
+    coverage_mask_kernel<kMaskMaxN><<<rows, 64, 0, stream>>>(a);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  coverage_fixup_kernel<<<rows, 64, 0, stream>>>(a);
+  if (a.nk <= kMaskSmallN) {
+    coverage_fixup_kernel<kMaskSmallN><<<rows, 64, 0, stream>>>(a);
+  } else {
+    coverage_fixup_kernel<kMaskMaxN><<<rows, 64, 0, stream>>>(a);
+  }
   return hipGetLastError();
 }
 

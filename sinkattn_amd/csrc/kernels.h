@@ -42,6 +42,7 @@ struct PoolArgs {
   const void* k;
   int64_t qs[4], ks[4];
   int B, H, Hk, Nq, Nk, nqb, nkb;
+  int bs, D;  // block size, head dim
   float scale;
   int causal;
   void* out;  // fp32 map (exact/mean) or q.dtype map (max)
@@ -114,6 +115,12 @@ int device_cu_count();
 int max_pool_groups();
 hipError_t launch_max_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_mean_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);
+// Any block size / head dim (pooling_generic.hip); LDS need, checked by the caller against
+// kGenericPoolMaxLds.
+constexpr size_t kGenericPoolMaxLds = 160 * 1024;
+size_t generic_pool_lds_need(int D, int nkb, int dtype);
+hipError_t launch_block_mass_generic(const PoolArgs& a, int dtype, hipStream_t stream);
+hipError_t launch_max_pool_generic(const PoolArgs& a, int dtype, hipStream_t stream);
 hipError_t launch_coverage_mask(const MaskArgs& a, hipStream_t stream);
 hipError_t launch_mean_pool_tokens(const TokenPoolArgs& a, int dtype, hipStream_t stream);
 hipError_t launch_lse_mix(const MixArgs& a, int dtype, hipStream_t stream);

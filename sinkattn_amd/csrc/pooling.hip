@@ -419,7 +419,7 @@ __global__ __launch_bounds__(128) void mean_pool_rows_kernel(PoolArgs a, int whi
   const int64_t* st = which == 0 ? a.qs : a.ks;
   const void* base = which == 0 ? a.q : a.k;
   const int D = blockDim.x;
-  const int bs = 128;
+  const int bs = a.bs;
   float acc = 0.f;
   for (int i = 0; i < bs; ++i) {
     const int n = min(blk * bs + i, N - 1);

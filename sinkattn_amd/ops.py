@@ -40,6 +40,17 @@ def _kernel_operand(t: torch.Tensor) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
+def _pad_head_dim(t: torch.Tensor) -> torch.Tensor:
+    """Zero-pad the head dim of a pooling operand to a multiple of 16 (16-bit dtypes: the
+    matrix-core score path) or 8 (fp32: the 8-element stride rule); dot products, the only
+    use of the head dim in the pooling modes, are unchanged by zero padding."""
+    D = int(t.shape[-1])
+    mult = 8 if t.dtype == torch.float32 else 16
+    if D % mult == 0:
+        return t
+    return torch.nn.functional.pad(t, (0, mult - D % mult))
+
+
 @dataclass
 class BlockSparsePlan:
     """Per-(b, h, q-block) ascending key-block lists built from a bool block mask."""
@@ -342,7 +353,8 @@ def block_mass_scores(q: torch.Tensor, k: torch.Tensor, block_size: int = 128,
     dt = _lib.dtype_code(q.dtype)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    qk, kk = _kernel_operand(q), _kernel_operand(k)
+    qk, kk = _kernel_operand(_pad_head_dim(q)), _kernel_operand(_pad_head_dim(k))
+    D = int(qk.shape[-1])
     out = torch.empty((B, H, _cdiv(Nq, block_size), _cdiv(Nk, block_size)), dtype=torch.float32,
                       device=q.device)
     L = _lib.lib()
@@ -402,7 +414,8 @@ def mean_pool_scores(q: torch.Tensor, k: torch.Tensor, block_size: int = 128,
     dt = _lib.dtype_code(q.dtype)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    qk, kk = _kernel_operand(q), _kernel_operand(k)
+    qk, kk = _kernel_operand(_pad_head_dim(q)), _kernel_operand(_pad_head_dim(k))
+    D = int(qk.shape[-1])
     L = _lib.lib()
     ws_bytes = int(L.sinkattn_mean_pool_workspace_bytes(B, H, Nq, Nk, D, int(block_size)))
     ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=q.device)

@@ -53,6 +53,8 @@ CONFIGS = [
     ("nodiag", (4, 40, 17), dict(keep_diagonal=False)),
     ("wide_rows", (2, 8, 600), {}),
     ("short_rows", (3, 9, 5), dict(coverage=0.5)),
+    ("long_rows", (2, 6, 2000), {}),  # past 1024 key blocks: the large-row kernels
+    ("max_rows", (1, 3, 4096), {}),
 ]
 
 
@@ -148,3 +150,25 @@ def test_calibrator_device_accumulation_is_bit_identical():
     assert torch.equal(pkg["mean_scores"]["0"], mean)
     assert torch.equal(pkg["std_scores"]["0"], std)
     assert torch.equal(pkg["sink_masks"]["0"], torch_ref.coverage_mask(mean))
+
+
+def test_calibrator_block_64_head_dim_64():
+    # block_size 64 and head dim 64 run the generic pooling kernel; the package's masks
+    # are the reference's mask of the package's own mean scores, and those means match the
+    # oracle's exact block mass of the recorded layers.
+    torch.manual_seed(2)
+    cfg = sa.SinkSparseConfig(pooling_mode="exact", block_size=64)
+    cal = sa.SinkMaskCalibrator(cfg)
+    qs, ks = [], []
+    for step in range(2):
+        q = torch.randn(2, 3, 700, 64, device="cuda", dtype=torch.bfloat16)
+        k = torch.randn(2, 3, 700, 64, device="cuda", dtype=torch.bfloat16)
+        cal.record(0, q, k, k)
+        qs.append(q.cpu())
+        ks.append(k.cpu())
+    pkg = cal.build_package()
+    mean = pkg["mean_scores"]["0"]
+    assert mean.shape == (3, 11, 11)
+    assert torch.equal(pkg["sink_masks"]["0"], torch_ref.coverage_mask(mean, block_size=64))
+    want = sum(torch_ref.exact_block_mass(q, k, block_size=64).mean(dim=0) for q, k in zip(qs, ks)) / 2
+    assert torch.allclose(mean, want, rtol=1e-5, atol=1e-8)

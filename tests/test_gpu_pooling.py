@@ -164,6 +164,65 @@ def test_attn_with_pooling_api_and_gqa():
     _max_pool_close(po, ref)
 
 
+def _qkd(B, H, Hk, Nq, Nk, D, dtype, seed, sinks=0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, Nq, D, generator=g)
+    k = torch.randn(B, Hk, Nk, D, generator=g)
+    if sinks:
+        k[:, :, :sinks] *= 6.0
+    return q.to(dtype), k.to(dtype)
+
+
+# Shapes off the block-128 / head-dim-128 MFMA kernels run on the generic kernels: block
+# sizes that do not divide 128 or exceed it, head dims 16..256, ragged ends, Nq != Nk, fp32
+# with more than 256 key blocks.
+@pytest.mark.parametrize("D,bs,Nq,Nk,dtype", [
+    (64, 64, 300, 300, torch.bfloat16), (128, 32, 260, 500, torch.bfloat16),
+    (32, 96, 333, 250, torch.float16), (256, 16, 200, 130, torch.float32),
+    (128, 256, 600, 600, torch.bfloat16), (80, 128, 300, 300, torch.bfloat16),
+    (128, 128, 200, 33000, torch.float32), (16, 7, 50, 61, torch.bfloat16),
+    (20, 64, 300, 280, torch.bfloat16), (20, 50, 300, 280, torch.float32)])
+def test_exact_mass_generic_shapes(D, bs, Nq, Nk, dtype):
+    q, k = _qkd(1, 2, 2, Nq, Nk, D, dtype, seed=D + bs, sinks=3)
+    ours = ops.block_mass_scores(q.cuda(), k.cuda(), block_size=bs)
+    ref = torch_ref.exact_block_mass(q, k, block_size=bs)
+    assert ours.shape == ref.shape
+    _close(ours, ref)
+    assert torch.allclose(ours.cpu().sum(-1), torch.ones(ref.shape[:-1]), atol=1e-5)
+
+
+@pytest.mark.parametrize("D,bs,N,dtype,causal", [
+    (64, 64, 500, torch.bfloat16, False), (64, 32, 333, torch.float16, True),
+    (256, 16, 200, torch.bfloat16, False), (32, 128, 400, torch.float32, False),
+    (128, 64, 1000, torch.bfloat16, True), (16, 16, 100, torch.bfloat16, False)])
+def test_max_pool_generic_shapes(D, bs, N, dtype, causal):
+    q, k = _qkd(1, 4, 2, N, N, D, dtype, seed=D * 7 + bs, sinks=2)  # GQA: 4 query heads, 2 kv
+    sm = 1.0 / math.sqrt(D)
+    ours = ops.max_pool_scores(q.cuda(), k.cuda(), sm, block_size=bs, causal=causal).cpu()
+    ref = torch_ref.max_pool_map(q, k, sm, block_size=bs, causal=causal)
+    assert ours.dtype == dtype and ours.shape == ref.shape
+    if dtype == torch.float32:
+        assert torch.allclose(ours, ref, rtol=1e-5, atol=1e-12)
+    else:
+        _max_pool_close(ours, ref, dtype, what=f"D={D} bs={bs}")
+
+
+def test_attn_with_pooling_block_64_head_dim_64():
+    from sinkattention.pooling_kernel import attn_with_pooling
+    q, k = _qkd(2, 3, 3, 640, 640, 64, torch.bfloat16, seed=21)
+    o, po = attn_with_pooling(q.cuda(), k.cuda(), k.cuda(), False, 0.125, 64)
+    assert o.shape == q.shape and not o.any() and po.shape == (2, 3, 10, 10)
+    _max_pool_close(po, torch_ref.max_pool_map(q, k, 0.125, block_size=64))
+
+
+@pytest.mark.parametrize("bs,D", [(64, 64), (200, 128), (16, 32), (64, 20)])
+def test_mean_mode_generic_block(bs, D):
+    q, k = _qkd(1, 2, 2, 700, 500, D, torch.bfloat16, seed=bs)
+    ours = ops.mean_pool_scores(q.cuda(), k.cuda(), block_size=bs).cpu()
+    ref = torch_ref.mean_pool_scores(q, k, block_size=bs)
+    assert torch.allclose(ours, ref, rtol=1e-5, atol=1e-7)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_mean_mode(dtype):
     q, k = _qk(2, 3, 1000, 700, dtype, seed=10)

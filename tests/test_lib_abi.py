@@ -85,13 +85,26 @@ def test_fwd_rejects_unaligned_or_strided_operands(lib):
 
 def test_pool_and_mask_validation(lib):
     s = _i64x4(0, 0, 128, 1)
-    assert lib.sinkattn_block_mass_pool(16, 16, 0, 1, 1, 128, 128, 128, s, s, 64, 1.0, 16, 16, None) < 0
+    assert lib.sinkattn_block_mass_pool(16, 16, 0, 1, 1, 128, 128, 128, s, s, 0, 1.0, 16, 16, None) < 0
     assert "block_size" in _err(lib)
-    assert lib.sinkattn_max_pool(16, 16, 2, 1, 1, 1, 128, 128, s, s, 128, 1.0, 0, 16, 16, None) < 0
+    # head dims above 256 only on the block-128 / head-dim-128 kernels' shapes
+    s512 = _i64x4(0, 0, 512, 1)
+    assert lib.sinkattn_block_mass_pool(16, 16, 0, 1, 1, 128, 128, 512, s512, s512, 64, 1.0, 16, 16, None) < 0
+    assert "256" in _err(lib)
+    # the generic kernels' LDS bounds the key-block count at a given head dim
+    assert lib.sinkattn_block_mass_pool(16, 16, 0, 1, 1, 16, 16 * 25000, 256, _i64x4(0, 0, 256, 1),
+                                        _i64x4(0, 0, 256, 1), 16, 1.0, 16, 16, None) < 0
+    assert "LDS" in _err(lib)
+    # max-pool keeps the reference's asserts on block size and head dim
+    assert lib.sinkattn_max_pool(16, 16, 2, 1, 1, 1, 128, 128, s, s, 48, 1.0, 0, 16, 16, None) < 0
+    assert "block_size" in _err(lib)
+    s96 = _i64x4(0, 0, 96, 1)
+    assert lib.sinkattn_max_pool(16, 16, 0, 1, 1, 1, 128, 96, s96, s96, 64, 1.0, 0, 16, 16, None) < 0
+    assert "head dim" in _err(lib)
     assert lib.sinkattn_max_pool(16, 16, 0, 1, 4, 3, 128, 128, s, s, 128, 1.0, 0, 16, 16, None) < 0
     assert "multiple" in _err(lib)
-    assert lib.sinkattn_coverage_mask(16, 1, 1, 2000, 0.85, 1, 0, 0, 0, 0, 16, None, None, 16, None) < 0
-    assert "1024" in _err(lib)
+    assert lib.sinkattn_coverage_mask(16, 1, 1, 5000, 0.85, 1, 0, 0, 0, 0, 16, None, None, 16, None) < 0
+    assert "4096" in _err(lib)
     assert lib.sinkattn_coverage_mask(16, 1, 1, 8, 0.85, 1, 0, 0, 5, 0, 16, None, None, 16, None) < 0
     assert "mode" in _err(lib)
     # empty problems are no-ops
