@@ -71,7 +71,7 @@ int sinkattn_block_sparse_plan(const uint8_t* mask, const int64_t mask_strides[4
  * A row with no listed key block gets out = 0 and lse = +inf.
  * counts/idx/order come from sinkattn_block_sparse_plan (order may be NULL: one
  * work-group per row in row order).
- * D must be 64 or 128.
+ * D must be 32, 64 or 128 (the head dims of the external kernel the reference calls).
  * ---------------------------------------------------------------------------------- */
 int sinkattn_block_sparse_fwd(const void* q, const void* k, const void* v, int dtype,
                               int64_t B, int64_t H, int64_t Nq, int64_t Nk, int64_t D,

@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_kernel(FwdArgs a) {
   const float c = a.scale * kLog2e;
 
   const int prow = k_row_perm(l32);
-  const int fk = k_swz(prow);
+  const int fk = k_swz_kc<D / 8>(prow);
 
   for (int it = 0; it < cnt; ++it) {
     const int kb = list[it];
@@ -478,7 +478,7 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_f32_kernel(FwdArgs a) {
   float m_run = neg_inf(), l_run = 0.f;
   const float c = a.scale * kLog2e;
   const int prow = k_row_perm(l32);
-  const int fk = k_swz(prow);
+  const int fk = k_swz_kc<KC>(prow);
 
   for (int it = 0; it < cnt; ++it) {
     const int key0 = list[it] * 128;
@@ -490,8 +490,8 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_f32_kernel(FwdArgs a) {
       const int key = key0 + row;
       u32x4 hi = u32x4{0, 0, 0, 0}, lo = u32x4{0, 0, 0, 0};
       if (key < a.Nk) split8(kbase + (int64_t)key * a.ks[2] + ch * 8, hi, lo);
-      kh[row * KC + (ch ^ k_swz(row))] = hi;
-      kl[row * KC + (ch ^ k_swz(row))] = lo;
+      kh[row * KC + (ch ^ k_swz_kc<KC>(row))] = hi;
+      kl[row * KC + (ch ^ k_swz_kc<KC>(row))] = lo;
     }
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) {
@@ -961,8 +961,10 @@ static hipError_t launch_fwd_dt(const FwdArgs& a, int D, hipStream_t stream) {
   const int grid = fwd_grid(a);
   if (D == 128)
     block_sparse_fwd_d128_kernel<CT><<<grid, 256, 0, stream>>>(a);
-  else
+  else if (D == 64)
     block_sparse_fwd_kernel<IT, CT, 64><<<grid, 256, 0, stream>>>(a);
+  else
+    block_sparse_fwd_kernel<IT, CT, 32><<<grid, 256, 0, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -975,8 +977,10 @@ hipError_t launch_block_sparse_fwd(const FwdArgs& a, int dtype, int D, hipStream
       const int grid = fwd_grid(a);
       if (D == 128)
         block_sparse_fwd_f32_kernel<128><<<grid, 256, 0, stream>>>(a);
-      else
+      else if (D == 64)
         block_sparse_fwd_f32_kernel<64><<<grid, 256, 0, stream>>>(a);
+      else
+        block_sparse_fwd_f32_kernel<32><<<grid, 256, 0, stream>>>(a);
       return hipGetLastError();
     }
   }

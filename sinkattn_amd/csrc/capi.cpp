@@ -104,7 +104,7 @@ int block_sparse_fwd_impl(const void* q, const void* k, const void* v, int dtype
                           const int32_t* idx, const int32_t* order, int64_t nqb, int64_t nkb,
                           float softmax_scale, const CompTiles& comp, void* stream) {
   if (!valid_dtype(dtype)) return fail("fwd: unsupported dtype %d", dtype);
-  if (D != 64 && D != 128) return fail("fwd: head dim %lld not supported (64 or 128)", (long long)D);
+  if (D != 32 && D != 64 && D != 128) return fail("fwd: head dim %lld not supported (32, 64 or 128)", (long long)D);
   if (B < 0 || H < 0 || Nq < 0 || Nk < 0) return fail("fwd: negative size");
   if (nqb != cdiv(Nq, 128) || nkb != cdiv(Nk, 128))
     return fail("fwd: plan is [%lld,%lld] blocks, expected [%lld,%lld]", (long long)nqb,

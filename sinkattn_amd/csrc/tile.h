@@ -15,6 +15,10 @@ __device__ __forceinline__ int k_row_perm(int r) {
   return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
 }
 __device__ __forceinline__ int k_swz(int row) { return (row & 3) | ((row >> 1) & 4); }
+// The K swizzle for rows of KC 16-byte chunks (head dim 8 KC): the same pattern, kept inside
+// the row when it has fewer than 8 chunks (head dim 32).
+template <int KC>
+__device__ __forceinline__ int k_swz_kc(int row) { return k_swz(row) & (KC - 1); }
 __device__ __forceinline__ int v_swz(int row) { return (row ^ (row >> 3)) & 7; }
 
 // Key offset (within a 32-key sub-tile) of accumulator register j of a lane in half hl.
@@ -37,7 +41,7 @@ __device__ __forceinline__ void stage_k_tile(u32x4* lds_k, const char* kbase, in
     const int key = key0 + row;
     u32x4 val = u32x4{0, 0, 0, 0};
     if (key < Nk) val = load8<IT, CT>(kbase + ((int64_t)key * ks2 + ch * 8) * ES);
-    lds_k[row * KC + (ch ^ k_swz(row))] = val;
+    lds_k[row * KC + (ch ^ k_swz_kc<KC>(row))] = val;
   }
 }
 

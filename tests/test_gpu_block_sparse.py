@@ -76,6 +76,19 @@ def test_small_random_masks(dtype, N):
     _check(out, lse, q, k, v, mask)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [32, 64])
+def test_head_dims_32_and_64(dtype, D):
+    # the register-staged kernel (head dims below 128; the external kernel the reference
+    # calls takes 32, 64 and 128), ragged N and Nq != Nk
+    q, _, _ = _inputs(2, 3, 700, 700, D, dtype, seed=D)
+    _, k, v = _inputs(2, 3, 900, 900, D, dtype, seed=D + 1, sink_keys=3)
+    mask = _random_mask(2, 3, 6, 8, 0.4, seed=D)
+    out, lse = ops.block_sparse_attention(q, k, v, ops.block_sparse_plan(mask))
+    torch.cuda.synchronize()
+    _check(out, lse, q, k, v, mask)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("step", [7.5, 30.0, -12.0])
 def test_running_maximum_moves_across_tiles(dtype, step):
