@@ -175,8 +175,8 @@ def cpu_baseline(torch, q, k, v, mask, n_qblocks, total_flops_layer):
 def main():
     args = _parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; the hot path is sharded by "
-                                   "(batch, head) with no collectives (see DESIGN.md), "
+        print(json.dumps({"error": "this build runs on one GPU only (across GPUs the hot path "
+                                   "would shard by (batch, head), with no collectives); "
                                    f"--gpus {args.gpus} is not supported"}))
         sys.exit(2)
     import torch
