@@ -230,3 +230,17 @@ def test_runtime_stats_density_is_cached_per_mask():
     st.record_mask_stats(layer_idx=0, sink_mask_tag="t", dynamic_mode="none", dynamic_sample_gap=1,
                          base_runtime_mask=m)
     assert len(calls) == 2 and st.sparsity_events[-1]["combined_density"] == 0.5
+
+
+def test_bench_refuses_more_than_one_gpu():
+    # one GPU only: --gpus N > 1 exits with status 2 and a JSON error line (before any GPU
+    # or torch work)
+    import json
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "4"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    msg = json.loads(r.stdout.strip().splitlines()[-1])
+    assert "one GPU" in msg["error"] and "--gpus 4" in msg["error"]
