@@ -60,18 +60,23 @@ def test_wan_layout_vs_oracle(dtype):
     _check(qn, _expect(q.cpu(), wq.cpu(), 1e-6, None, None, H, D, dtype), dtype, f"norm only {dtype}")
 
 
-def test_zimage_layout_per_batch_tables_vs_oracle():
-    B, N, H, D = 2, 700, 6, 128
+# Rows of one head share their position's table row.  6 heads in bf16 take the row-walk
+# kernel; 30 heads (Z-Image's), and fp32 rows of 4 lanes' worth, take the position-major one
+# (a position's rows in steps of 64 / lanes-per-row, the table entries loaded once).
+@pytest.mark.parametrize("H,dtype", [(6, torch.bfloat16), (30, torch.bfloat16), (30, torch.float16),
+                                     (30, torch.float32), (9, torch.float32)])
+def test_zimage_layout_per_batch_tables_vs_oracle(H, dtype):
+    B, N, D = 2, 700, 128
     g = torch.Generator(device=DEV).manual_seed(2)
-    q = torch.randn(B, N, H, D, device=DEV, generator=g).to(torch.bfloat16)
-    k = torch.randn(B, N, H, D, device=DEV, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, N, H, D, device=DEV, generator=g).to(dtype)
+    k = torch.randn(B, N, H, D, device=DEV, generator=g).to(dtype)
     wq, wk = torch.rand(D, device=DEV) + 0.5, torch.rand(D, device=DEV) + 0.5
     ang = torch.randn(B, N, D // 2, device=DEV)
     f = torch.polar(torch.ones_like(ang), ang)
     qo, ko = ops.qk_norm_rotary(q, k, wq, wk, 1e-5, 1e-5, D, f.real, f.imag, rows_per_pos=H)
     re, im = f.real.cpu()[:, :, None, None, :], f.imag.cpu()[:, :, None, None, :]
-    _check(qo, _expect(q.cpu(), wq.cpu(), 1e-5, re, im, 1, D, torch.bfloat16), torch.bfloat16, "zimage q")
-    _check(ko, _expect(k.cpu(), wk.cpu(), 1e-5, re, im, 1, D, torch.bfloat16), torch.bfloat16, "zimage k")
+    _check(qo, _expect(q.cpu(), wq.cpu(), 1e-5, re, im, 1, D, dtype), dtype, f"zimage q H={H} {dtype}")
+    _check(ko, _expect(k.cpu(), wk.cpu(), 1e-5, re, im, 1, D, dtype), dtype, f"zimage k H={H} {dtype}")
 
 
 def test_errors():
