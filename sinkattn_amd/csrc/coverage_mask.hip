@@ -11,8 +11,9 @@
 //   * `coverage * total` is one fp32 multiply; comparisons with 1e-6 are fp32;
 //   * `torch.sort(descending=True)` is libstdc++ `std::sort` on (value, index) pairs with
 //     comparator `(isnan(a) && !isnan(b)) || a > b` (unstable).
-// One 64-thread work-group handles one (head, query-block) row.  The row is sorted with
-// a bitonic network keyed (value desc, index asc).  Values, prefix sums and the cut k
+// One 64-thread work-group handles one (head, query-block) row.  The row sums run ATen's
+// 32 accumulator chains one per lane; the row is sorted with a register-resident bitonic
+// network keyed (value desc, index asc).  Values, prefix sums and the cut k
 // do not depend on how ties are ordered; the selected set does only when a tie group
 // straddles the cut (v[k-1] == v[k]) or the empty-row fallback picks among tied maxima.
 // Those rows are re-sorted with a single-lane emulation of libstdc++'s introsort so the
@@ -29,9 +30,8 @@
 
 namespace sa {
 
-// Row capacities: rows of up to 1024 key blocks use the small instance (21 KB of LDS),
-// longer rows (up to 4096) the large one (84 KB, one work-group per CU).
-constexpr int kMaskSmallN = 1024;
+// Row capacity: instances hold rows of 256 * C key blocks for C = 1, 2, 4, 8, 16 (5.3 KB
+// to 84 KB of LDS), so short rows keep many work-groups resident per CU.
 constexpr int kMaskMaxN = 4096;
 
 // --- ATen-compatible fp32 row sum ---------------------------------------------------
@@ -296,6 +296,129 @@ __device__ void std_sort(const PairArr& p, int n) {
   }
 }
 
+// --- wave-parallel ATen row sum ------------------------------------------------------
+// The vectorised inner sum above keeps 32 independent fp32 chains, accumulator k of lane
+// e for k < 4, e < 8; each chain's adds (and the cascade that folds its levels) depend
+// only on the unit counter.  Here each chain runs in its own wave lane (lane bits 3-4 = k,
+// bits 0-2 = e) and the folds across chains happen in ATen's order through cross-lane
+// reads, so every rounding is the one of the serial form.  The two half-waves sum with
+// different RowViews (plain and required-masked).  Needs n >= 8; the result is returned
+// in every lane of the half-wave.
+__device__ __forceinline__ float aten_row_sum_wave(const RowView& r, int lane) {
+  const int n = r.n;
+  const int nunits = n / 8;
+  const int half = lane >> 5, kq = (lane >> 3) & 3, e = lane & 7;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  const int size_ilp = nunits / 4;
+  const int level_power = max(4, ceil_log2(size_ilp) / 4);
+  const int level_step = 1 << level_power;
+  const int level_mask = level_step - 1;
+  int i = 0;
+  while (i + level_step <= size_ilp) {
+    for (int j = 0; j < level_step; ++j, ++i) a0 += r.at((i * 4 + kq) * 8 + e);
+    a1 += a0;
+    a0 = 0.f;
+    if ((i & (level_mask << level_power)) == 0) {
+      a2 += a1;
+      a1 = 0.f;
+      if ((i & (level_mask << (2 * level_power))) == 0) {
+        a3 += a2;
+        a2 = 0.f;
+      }
+    }
+  }
+  for (; i < size_ilp; ++i) a0 += r.at((i * 4 + kq) * 8 + e);
+  a0 += a1;
+  a0 += a2;
+  a0 += a3;
+  if (kq == 0)
+    for (int v = size_ilp * 4; v < nunits; ++v) a0 += r.at(v * 8 + e);
+  // Accumulators 1..3 into 0, in order (meaningful in the kq == 0 lanes).
+  const float b1 = __shfl(a0, lane + 8), b2 = __shfl(a0, lane + 16), b3 = __shfl(a0, lane + 24);
+  const float lane_sum = ((a0 + b1) + b2) + b3;
+  float fin = 0.f;
+  for (int t = nunits * 8; t < n; ++t) fin += r.at(t);
+#pragma unroll
+  for (int ee = 0; ee < 8; ++ee) fin += __shfl(lane_sum, (half << 5) + ee);
+  return fin;
+}
+
+// --- cross-lane moves -------------------------------------------------------------------
+// DPP controls (gfx9 encoding): quad_perm 0x00-0xff, row_shr:n 0x110+n, row_ror:n 0x120+n,
+// row_bcast:15 0x142, row_bcast:31 0x143.  Lanes without a source (or outside ROW_MASK)
+// keep `old`.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+
+// Inclusive scans over the 64 lanes: row_shr 1, 2, 4, 8 inside each 16-lane row, then the
+// row totals carried by row_bcast:15 (into rows 1 and 3) and row_bcast:31 (rows 2 and 3).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_f64_or_zero(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = dpp_u32<CTRL, ROW_MASK>(0u, (uint32_t)b);
+  const uint32_t hi = dpp_u32<CTRL, ROW_MASK>(0u, (uint32_t)(b >> 32));
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double wave_scan_add_f64(double v) {
+  v += dpp_f64_or_zero<0x111, 0xf>(v);
+  v += dpp_f64_or_zero<0x112, 0xf>(v);
+  v += dpp_f64_or_zero<0x114, 0xf>(v);
+  v += dpp_f64_or_zero<0x118, 0xf>(v);
+  v += dpp_f64_or_zero<0x142, 0xa>(v);
+  v += dpp_f64_or_zero<0x143, 0xc>(v);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_scan_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0x111, 0xf>(0u, v));
+  v = max(v, dpp_u32<0x112, 0xf>(0u, v));
+  v = max(v, dpp_u32<0x114, 0xf>(0u, v));
+  v = max(v, dpp_u32<0x118, 0xf>(0u, v));
+  v = max(v, dpp_u32<0x142, 0xa>(0u, v));
+  v = max(v, dpp_u32<0x143, 0xc>(0u, v));
+  return v;
+}
+__device__ __forceinline__ int wave_scan_min_i32(int v) {
+  constexpr uint32_t kId = 0x7fffffffu;
+  v = min(v, (int)dpp_u32<0x111, 0xf>(kId, (uint32_t)v));
+  v = min(v, (int)dpp_u32<0x112, 0xf>(kId, (uint32_t)v));
+  v = min(v, (int)dpp_u32<0x114, 0xf>(kId, (uint32_t)v));
+  v = min(v, (int)dpp_u32<0x118, 0xf>(kId, (uint32_t)v));
+  v = min(v, (int)dpp_u32<0x142, 0xa>(kId, (uint32_t)v));
+  v = min(v, (int)dpp_u32<0x143, 0xc>(kId, (uint32_t)v));
+  return v;
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Value of lane `lane ^ M` (M = 1, 2, 4, 8: DPP; 16: ds_bpermute; 32: v_permlane32_swap).
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v, int lane) {
+  if constexpr (M == 1) {
+    return dpp_u32<0xb1, 0xf>(v, v);  // quad_perm [1,0,3,2]
+  } else if constexpr (M == 2) {
+    return dpp_u32<0x4e, 0xf>(v, v);  // quad_perm [2,3,0,1]
+  } else if constexpr (M == 4) {
+    const uint32_t up = dpp_u32<0x12c, 0xf>(v, v);    // row_ror:12 -> lane + 4 (mod 16)
+    const uint32_t down = dpp_u32<0x124, 0xf>(v, v);  // row_ror:4  -> lane - 4 (mod 16)
+    return (lane & 4) ? down : up;
+  } else if constexpr (M == 8) {
+    return dpp_u32<0x128, 0xf>(v, v);  // row_ror:8 -> lane ^ 8
+  } else if constexpr (M == 16) {
+    return (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ 16) << 2, (int)v);
+  } else {
+    static_assert(M == 32, "lane distance");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  }
+}
+
 // --- bitonic sort keys ------------------------------------------------------------------
 __device__ __forceinline__ uint32_t order_key(float x) {
   if (__builtin_isnan(x)) return 0xffffffffu;
@@ -304,14 +427,122 @@ __device__ __forceinline__ uint32_t order_key(float x) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-template <int NMAX>
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src_lane_x4) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane_x4, (int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane_x4, (int)(uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Descending bitonic sort of 256*C distinct 64-bit keys held in registers: key (c, r) of
+// lane l is element j = c*256 + l*4 + r.  Distances 1 and 2 stay inside a lane, 4..128
+// cross lanes (ds_bpermute), 256 and up cross a lane's own chunks.  A compare-exchange
+// leaves the larger key at the lower index inside blocks whose `size` bit of j is clear
+// and the smaller one where it is set, so the full network ends in descending order.
+template <int C, int D>
+__device__ __forceinline__ void chunk_stage(uint64_t (&kk)[C][4], int size) {
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    if ((c & D) == 0) {
+      const bool desc = ((c << 8) & size) == 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint64_t x = kk[c][r], y = kk[c | D][r];
+        const bool sw = (x < y) == desc;
+        kk[c][r] = sw ? y : x;
+        kk[c | D][r] = sw ? x : y;
+      }
+    }
+  }
+}
+
+// Distances 4..128: lane l pairs with lane l ^ M (M = distance / 4).
+template <int C, int M>
+__device__ __forceinline__ void xlane_stage(uint64_t (&kk)[C][4], int size, int lane) {
+  const bool lo = (lane & M) == 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const bool desc = ((((c << 8) | (lane << 2))) & size) == 0;
+    const bool want_max = lo == desc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint64_t x = kk[c][r];
+      const uint64_t y = ((uint64_t)xor_lane<M>((uint32_t)(x >> 32), lane) << 32) |
+                         xor_lane<M>((uint32_t)x, lane);
+      const bool take_y = want_max ? (y > x) : (y < x);
+      kk[c][r] = take_y ? y : x;
+    }
+  }
+}
+
+// Distances 1 and 2: pairs inside a lane.
+template <int C, int S>
+__device__ __forceinline__ void lane_stage(uint64_t (&kk)[C][4], int size, int lane) {
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if ((r & S) == 0) {
+        const bool desc = ((((c << 8) | (lane << 2) | r)) & size) == 0;
+        const uint64_t x = kk[c][r], y = kk[c][r | S];
+        const bool sw = (x < y) == desc;
+        kk[c][r] = sw ? y : x;
+        kk[c][r | S] = sw ? x : y;
+      }
+    }
+  }
+}
+
+template <int C>
+__device__ __forceinline__ void bitonic_sort_regs(uint64_t (&kk)[C][4], int lane) {
+  constexpr int P = 256 * C;
+  for (int size = 2; size <= P; size <<= 1) {
+    // Distances of 256 and up, longest first, each chunk distance a compile-time constant
+    // (as separate steps rather than one indexed step, so every key stays in a register).
+    if constexpr (C >= 16) {
+      if (size >= 4096) chunk_stage<C, 8>(kk, size);
+    }
+    if constexpr (C >= 8) {
+      if (size >= 2048) chunk_stage<C, 4>(kk, size);
+    }
+    if constexpr (C >= 4) {
+      if (size >= 1024) chunk_stage<C, 2>(kk, size);
+    }
+    if constexpr (C >= 2) {
+      if (size >= 512) chunk_stage<C, 1>(kk, size);
+    }
+    for (int stride = min(size >> 1, 128); stride >= 4; stride >>= 1) {
+      switch (stride) {
+        case 128: xlane_stage<C, 32>(kk, size, lane); break;
+        case 64: xlane_stage<C, 16>(kk, size, lane); break;
+        case 32: xlane_stage<C, 8>(kk, size, lane); break;
+        case 16: xlane_stage<C, 4>(kk, size, lane); break;
+        case 8: xlane_stage<C, 2>(kk, size, lane); break;
+        default: xlane_stage<C, 1>(kk, size, lane); break;
+      }
+    }
+    if (size >= 4) lane_stage<C, 2>(kk, size, lane);
+    lane_stage<C, 1>(kk, size, lane);
+  }
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const uint64_t o = shfl_u64(v, ((int)(threadIdx.x & 63) ^ m) << 2);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// One 64-thread work-group per (head, query-block) row; rows of up to 256*C key blocks.
+template <int C>
 __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
+  constexpr int NMAX = 256 * C;
   __shared__ float row[NMAX];
   __shared__ unsigned long long keys[NMAX];
-  __shared__ float sv[NMAX];    // sorted values (tie-exact order when needed)
-  __shared__ int si[NMAX];      // sorted indices
+  __shared__ __attribute__((aligned(16))) float sv[NMAX];  // sorted values (tie-exact order when needed)
+  __shared__ int si[NMAX];                                // sorted indices
   __shared__ uint8_t m[NMAX];
-  __shared__ float sums_sh[2];
   __shared__ int k_sh, exact_sh;
 
   const int lane = threadIdx.x;
@@ -327,106 +558,181 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
   const int n = video ? max(nk - tb, 0) : nk;
   const bool video_row = video && qb >= tb && n > 0 && (a.nq - tb) > 0;
 
-  for (int j = lane; j < nk; j += 64) {
-    row[j] = src[j];
-    const bool req = (qb < a.req_q) || (j < a.req_k);
-    m[j] = req ? 1 : 0;
+  // Row into LDS, all loads of a lane issued before the first store.
+  {
+    constexpr int NL = 4 * C;
+    constexpr int NB = NL < 8 ? NL : 8;
+#pragma unroll
+    for (int i0 = 0; i0 < NL; i0 += NB) {
+      float v[NB];
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const int j = (i0 + u) * 64 + lane;
+        v[u] = j < nk ? src[j] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const int j = (i0 + u) * 64 + lane;
+        if (j < nk) {
+          row[j] = v[u];
+          m[j] = ((qb < a.req_q) || (j < a.req_k)) ? 1 : 0;
+        }
+      }
+    }
   }
   __syncthreads();
 
-  // Sums: lane 0 plain total, lane 1 required-masked total (joint) -- same code path.
-  if (lane < 2) {
+  // Sums: half-wave 0 the plain total, half-wave 1 the required-masked total (joint).
+  float sum_plain = 0.f, sum_req = 0.f;
+  if (!video || video_row) {
     RowView rv;
     rv.x = row + off;
     rv.n = n;
     rv.qb = qb;
     rv.req_q = a.req_q;
     rv.req_k = video ? 0 : a.req_k;
-    rv.masked = (lane == 1) && !video;
-    const float s = (!video || video_row) ? aten_row_sum(rv) : 0.f;
-    sums_sh[lane] = s;
+    rv.masked = (lane >= 32) && !video;
+    float s;
+    if (n >= 8) {
+      s = aten_row_sum_wave(rv, lane);
+    } else {
+      float one[1];
+      aten_units_sum<1>(rv, n, one);
+      s = one[0];
+    }
+    sum_plain = __shfl(s, 0);
+    sum_req = __shfl(s, 32);
   }
-  __syncthreads();
 
   const bool do_select = video ? video_row : true;
   float target = 0.f;
+  int exact = 0;
   if (do_select) {
-    float total = sums_sh[0];
+    float total = sum_plain;
     total = (total < 1e-6f) ? 1e-6f : total;  // clamp_min_ (NaN propagates)
     const float tgt = a.coverage * total;
     if (video) {
       target = tgt;
     } else {
-      float res = tgt - sums_sh[1];
+      float res = tgt - sum_req;
       target = (res < 0.f) ? 0.f : res;
     }
-    // Candidate keys.
-    int P = 1;
-    while (P < n) P <<= 1;
-    for (int j = lane; j < P; j += 64) {
-      unsigned long long key = 0ull;
-      if (j < n) {
-        const float x = row[off + j];
-        const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
-        const float cv = req ? neg_inf() : x;
-        key = ((unsigned long long)order_key(cv) << 32) | (unsigned long long)(~(uint32_t)j);
-      }
-      keys[j] = key;
-    }
-    __syncthreads();
-    // Bitonic sort, descending.
-    for (int size = 2; size <= P; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int t = lane; t < P / 2; t += 64) {
-          const int lo = 2 * t - (t & (stride - 1));
-          const int hi = lo + stride;
-          const bool desc = ((lo & size) == 0);
-          const unsigned long long x = keys[lo], y = keys[hi];
-          if ((x < y) == desc) {
-            keys[lo] = y;
-            keys[hi] = x;
-          }
+    // Candidate keys (value desc, index asc); positions past n hold 0, below every key.
+    uint64_t kk[C][4];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = c * 256 + lane * 4 + r;
+        uint64_t key = 0ull;
+        if (j < n) {
+          const float x = row[off + j];
+          const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
+          const float cv = req ? neg_inf() : x;
+          key = ((uint64_t)order_key(cv) << 32) | (uint64_t)(~(uint32_t)j);
         }
-        __syncthreads();
+        kk[c][r] = key;
       }
-    }
-    for (int j = lane; j < n; j += 64) {
-      const int id = (int)(~(uint32_t)(keys[j] & 0xffffffffull));
-      si[j] = id;
-      const bool req = !video && ((qb < a.req_q) || (id < a.req_k));
-      sv[j] = req ? neg_inf() : row[off + id];
-    }
+    bitonic_sort_regs<C>(kk, lane);
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = c * 256 + lane * 4 + r;
+        keys[j] = kk[c][r];
+        if (j < n) {
+          const int id = (int)(~(uint32_t)(kk[c][r] & 0xffffffffull));
+          si[j] = id;
+          const bool req = !video && ((qb < a.req_q) || (id < a.req_k));
+          sv[j] = req ? neg_inf() : row[off + id];
+        }
+      }
     __syncthreads();
 
-    if (lane == 0) {
-      // Prefix sums in fp64, each rounded to fp32, first index reaching the target.
-      double cum = 0.0;
-      int first = -1;
-      for (int i = 0; i < n; ++i) {
-        float x = sv[i];
+    // Prefix sums in fp64, each rounded to fp32: the first index reaching the target.
+    // A prefix x[0..j] whose partial sums are all exact in fp64 gives the same sums in any
+    // order: every partial sum is a multiple of 2^lsb_min (the lowest set bit over the
+    // prefix) no larger than (j+1) * max|x| < 2^(ceil(log2(j+1)) + e(max|x|) + 1), exact
+    // while that is at most 2^(lsb_min + 52).  Such prefixes are scanned 64 at a time
+    // across the wave; from the first index past that bound (or a non-finite value) lane 0
+    // continues the serial walk from the exact sum before it.
+    int first = -1;
+    {
+      double base = 0.0;
+      uint32_t run_max = 0u;    // max |x| (bits) so far
+      int run_lsb = 0x7fffffff;  // lowest set-bit exponent so far
+      int serial_from = -1;
+      double serial_cum = 0.0;
+      for (int c0 = 0; c0 < n; c0 += 64) {
+        const int j = c0 + lane;
+        float x = j < n ? sv[j] : 0.f;
         if (!video && !__builtin_isfinite(x)) x = 0.f;
-        cum += (double)x;
-        if (first < 0 && (float)cum >= target) first = i;
+        const uint32_t ab = __float_as_uint(x) & 0x7fffffffu;
+        int lsb = 0x7fffffff;
+        if (ab != 0u && ab < 0x7f800000u) {
+          const uint32_t E = ab >> 23, mant = ab & 0x7fffffu;
+          const uint32_t sig = E ? (mant | 0x800000u) : mant;
+          lsb = (int)(E ? E : 1u) - 150 + __builtin_ctz(sig);
+        }
+        const uint32_t mx = max(run_max, wave_scan_max_u32(ab));
+        const int mn = min(run_lsb, wave_scan_min_i32(lsb));
+        bool ok;
+        if (mx >= 0x7f800000u) {
+          ok = false;  // inf or NaN in the prefix
+        } else if (mx == 0u) {
+          ok = true;
+        } else {
+          const int eM = (mx >> 23) ? (int)(mx >> 23) - 127 : -149 + (31 - __builtin_clz(mx));
+          const int cl = j == 0 ? 0 : 32 - __builtin_clz((uint32_t)j);  // ceil(log2(j + 1))
+          ok = cl + eM + 1 <= mn + 52;
+        }
+        const double S = base + wave_scan_add_f64((double)x);
+        const bool valid = j < n;
+        const uint64_t hits = __ballot(valid && ok && (float)S >= target);
+        if (hits) {
+          first = c0 + __builtin_ctzll(hits);
+          break;
+        }
+        const uint64_t bad = __ballot(valid && !ok);
+        if (bad) {
+          const int f = __builtin_ctzll(bad);
+          serial_from = c0 + f;
+          serial_cum = f == 0 ? base : readlane_f64(S, f - 1);
+          break;
+        }
+        base = readlane_f64(S, 63);
+        run_max = (uint32_t)__builtin_amdgcn_readlane((int)mx, 63);
+        run_lsb = __builtin_amdgcn_readlane(mn, 63);
       }
-      int ncand = 0;
-      if (video) {
-        ncand = n;
-      } else {
-        for (int j = 0; j < n; ++j) ncand += ((qb < a.req_q) || (j < a.req_k)) ? 0 : 1;
+      if (serial_from >= 0 && lane == 0) {
+        double cum = serial_cum;
+        for (int i = serial_from; i < n; ++i) {
+          float x = sv[i];
+          if (!video && !__builtin_isfinite(x)) x = 0.f;
+          cum += (double)x;
+          if ((float)cum >= target) {
+            first = i;
+            break;
+          }
+        }
       }
+    }
+    if (lane == 0) {
+      const int ncand = video ? n : ((qb < a.req_q) ? 0 : n - min(a.req_k, n));
       int k = target > 1e-6f ? (first >= 0 ? first + 1 : ncand) : 0;
       k = min(max(k, 0), n);
-      int exact = 0;
-      if (k > 0 && k < n && (keys[k - 1] >> 32) == (keys[k] >> 32)) exact = 1;
+      int ex = 0;
+      if (k > 0 && k < n && (keys[k - 1] >> 32) == (keys[k] >> 32)) ex = 1;
       k_sh = k;
-      exact_sh = exact;
+      exact_sh = ex;
     }
     __syncthreads();
+    exact = exact_sh;
   }
 
   const int k = do_select ? k_sh : 0;
   // Exact permutation for rows whose selection depends on the order of tied values.
-  auto run_exact = [&]() {
+  if (do_select && exact) {
     if (lane == 0) {
       for (int j = 0; j < n; ++j) {
         const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
@@ -437,8 +743,7 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
       std_sort(p, n);
     }
     __syncthreads();
-  };
-  if (do_select && exact_sh) run_exact();
+  }
 
   for (int i = lane; i < k; i += 64) m[off + si[i]] = 1;
   __syncthreads();
@@ -453,19 +758,22 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
   any = __any(any);
   uint8_t* mrow = a.mask + (int64_t)rid * nk;
   for (int j = lane; j < nk; j += 64) mrow[j] = m[j];
-  if (lane == 0) {
-    int top1 = 0, tie = 0;
-    if (video) {  // scores.argmax(dim=-1): first maximum of the full row, NaN maximal
-      float bv = row[0];
-      for (int j = 1; j < nk; ++j) {
-        const float x = row[j];
-        if (__builtin_isnan(bv)) break;
-        if (__builtin_isnan(x) || x > bv) { bv = x; top1 = j; }
-      }
-    } else {  // sorted_indices[..., 0]
-      top1 = si[0];
-      tie = (!exact_sh && n > 1 && (keys[0] >> 32) == (keys[1] >> 32)) ? 1 : 0;
+  int top1 = 0, tie = 0;
+  if (video) {
+    // scores.argmax(dim=-1): the first NaN if there is one, else the first maximum
+    // (-0 == +0) -- the largest (order_key(x), ~j) over the full row.
+    uint64_t best = 0ull;
+    for (int j = lane; j < nk; j += 64) {
+      const uint64_t key = ((uint64_t)order_key(row[j]) << 32) | (uint64_t)(~(uint32_t)j);
+      best = key > best ? key : best;
     }
+    best = wave_max_u64(best);
+    top1 = (int)(~(uint32_t)(best & 0xffffffffull));
+  } else if (lane == 0) {  // sorted_indices[..., 0]
+    top1 = si[0];
+    tie = (!exact && n > 1 && (keys[0] >> 32) == (keys[1] >> 32)) ? 1 : 0;
+  }
+  if (lane == 0) {
     a.ws_top1[rid] = top1;
     a.ws_flags[rid] = (uint8_t)((any ? 0 : 1) | (tie << 1));
   }
@@ -476,8 +784,9 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
 // 371-374) runs when ANY row of the tensor is empty and then sets mask[r, top1[r]] =
 // empty[r] for EVERY row r -- it also clears the top-1 bit of non-empty rows.  Then the
 // ascending index lists and counts of the final mask are written.
-template <int NMAX>
+template <int C>
 __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
+  constexpr int NMAX = 256 * C;
   __shared__ float sv[NMAX];
   __shared__ int si[NMAX];
   __shared__ uint8_t m[NMAX];
@@ -486,13 +795,33 @@ __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
   const int rows = a.H * a.nq;
   const int qb = rid % a.nq;
   const int nk = a.nk;
-  int any_empty = 0;
-  for (int i = lane; i < rows; i += 64) any_empty |= a.ws_flags[i] & 1;
-  any_empty = __any(any_empty);
+  // Empty flags (bit 0 of each byte), four rows per 32-bit word; the flag region is
+  // padded to 256 bytes, and bytes past `rows` are masked off.
+  uint32_t any_empty = 0;
+  {
+    const uint32_t* fw = reinterpret_cast<const uint32_t*>(a.ws_flags);
+    const int words = (rows + 3) >> 2;
+    for (int w0 = 0; w0 < words; w0 += 64 * 8) {
+      uint32_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int w = w0 + u * 64 + lane;
+        v[u] = w < words ? fw[w] : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int w = w0 + u * 64 + lane;
+        const int left = rows - 4 * w;  // rows held by this word
+        const uint32_t keep = left >= 4 ? 0x01010101u : (left == 3 ? 0x010101u : (left == 2 ? 0x0101u : 0x01u));
+        any_empty |= v[u] & keep;
+      }
+    }
+  }
+  const bool fallback = __any(any_empty != 0);
   uint8_t* mrow = a.mask + (int64_t)rid * nk;
   for (int j = lane; j < nk; j += 64) m[j] = mrow[j];
   __syncthreads();
-  if (any_empty) {
+  if (fallback) {
     const uint8_t flags = a.ws_flags[rid];
     if (lane == 0) {
       int t = a.ws_top1[rid];
@@ -526,22 +855,24 @@ __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
   }
 }
 
+template <int C>
+static hipError_t launch_mask_c(const MaskArgs& a, int rows, hipStream_t stream) {
+  coverage_mask_kernel<C><<<rows, 64, 0, stream>>>(a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  coverage_fixup_kernel<C><<<rows, 64, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
 hipError_t launch_coverage_mask(const MaskArgs& a, hipStream_t stream) {
   const int rows = a.H * a.nq;
   if (rows == 0 || a.nk == 0) return hipSuccess;
-  if (a.nk <= kMaskSmallN) {
-    coverage_mask_kernel<kMaskSmallN><<<rows, 64, 0, stream>>>(a);
-  } else {
-    coverage_mask_kernel<kMaskMaxN><<<rows, 64, 0, stream>>>(a);
-  }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (a.nk <= kMaskSmallN) {
-    coverage_fixup_kernel<kMaskSmallN><<<rows, 64, 0, stream>>>(a);
-  } else {
-    coverage_fixup_kernel<kMaskMaxN><<<rows, 64, 0, stream>>>(a);
-  }
-  return hipGetLastError();
+  if (a.nk > kMaskMaxN) return hipErrorInvalidValue;
+  if (a.nk <= 256) return launch_mask_c<1>(a, rows, stream);
+  if (a.nk <= 512) return launch_mask_c<2>(a, rows, stream);
+  if (a.nk <= 1024) return launch_mask_c<4>(a, rows, stream);
+  if (a.nk <= 2048) return launch_mask_c<8>(a, rows, stream);
+  return launch_mask_c<16>(a, rows, stream);
 }
 
 }  // namespace sa

@@ -53,7 +53,10 @@ CONFIGS = [
     ("nodiag", (4, 40, 17), dict(keep_diagonal=False)),
     ("wide_rows", (2, 8, 600), {}),
     ("short_rows", (3, 9, 5), dict(coverage=0.5)),
-    ("long_rows", (2, 6, 2000), {}),  # past 1024 key blocks: the large-row kernels
+    ("mid_rows", (2, 7, 300), {}),  # one kernel instance per power-of-two row capacity
+    ("rows_1024", (1, 4, 1024), {}),
+    ("video_long", (2, 10, 700), dict(text_length=512, force_text=True, mode="video_residual")),
+    ("long_rows", (2, 6, 2000), {}),
     ("max_rows", (1, 3, 4096), {}),
 ]
 
@@ -172,3 +175,70 @@ def test_calibrator_block_64_head_dim_64():
     assert torch.equal(pkg["sink_masks"]["0"], torch_ref.coverage_mask(mean, block_size=64))
     want = sum(torch_ref.exact_block_mass(q, k, block_size=64).mean(dim=0) for q, k in zip(qs, ks)) / 2
     assert torch.allclose(mean, want, rtol=1e-5, atol=1e-8)
+
+
+def _serial_walk_rows(s, coverage):
+    """Rows whose coverage cut lies past the range where fp64 prefix sums are exact in any
+    order (the kernel scans that range across the wave and walks the rest serially):
+    restated from the bound the kernel documents, to show these inputs reach the walk."""
+    x = np.sort(s.reshape(-1, s.shape[-1]).astype(np.float32), axis=-1)[:, ::-1]
+    count = 0
+    for row in x:
+        tot = max(np.float32(row.sum(dtype=np.float32)), np.float32(1e-6))
+        cum = np.cumsum(row.astype(np.float64)).astype(np.float32)
+        hit = np.nonzero(cum >= np.float32(coverage) * tot)[0]
+        cut = hit[0] if hit.size else len(row)
+        ab = np.abs(row.astype(np.float64))
+        mant, ex = np.frexp(np.where(ab > 0, ab, 1.0))  # v = mant * 2^ex, mant in [0.5, 1)
+        sig = (mant * 2.0 ** 24).astype(np.int64)  # 24-bit significand as an integer
+        tz = np.log2(sig & -sig).astype(np.int64)
+        lsb = np.where(ab > 0, ex - 24 + tz, 1 << 20)
+        top = np.where(ab > 0, ex - 1, -(1 << 20))  # floor(log2 |x|)
+        lsb_min = np.minimum.accumulate(lsb)
+        e_max = np.maximum.accumulate(top)
+        j = np.arange(len(row))
+        cl = np.ceil(np.log2(j + 1)).astype(np.int64)
+        bad = np.nonzero((e_max > -(1 << 20)) & (cl + e_max + 1 > lsb_min + 52))[0]
+        if bad.size and bad[0] <= cut:
+            count += 1
+    return count
+
+
+@pytest.mark.parametrize("coverage,alpha", [(1.0, 0.02), (0.9999999, 0.02)])
+def test_prefix_walk_past_exact_range(oracle_lib, coverage, alpha):
+    # Wide dynamic range (gamma draws down to denormals) with the cut in the tail: the
+    # prefix sums leave the exact range before the cut, so the serial walk finishes them.
+    rng = np.random.default_rng(11)
+    x = rng.gamma(alpha, size=(3 * 40, 300)).astype(np.float32)
+    x[:, 7] += 0.5
+    s = torch.from_numpy(x).view(3, 40, 300)
+    s = s / s.sum(-1, keepdim=True)
+    assert _serial_walk_rows(s.numpy(), coverage) > 10
+    ref = torch_ref.coverage_mask(s, coverage=coverage)
+    got, counts, idx = ops.coverage_mask(s.cuda(), coverage, True, want_lists=True)
+    assert torch.equal(got.cpu(), ref)
+    _check_lists(got, counts, idx)
+    assert np.array_equal(oracle_lib.coverage_mask(s.numpy(), coverage), ref.numpy())
+
+
+@pytest.mark.parametrize("mode", ["joint", "video_residual"])
+def test_non_finite_scores(mode):
+    # inf and NaN entries: NaN sorts first, non-finite values count as 0 in the joint
+    # prefix sums, and the video branch's sums and argmax carry them as CPU torch does.
+    rng = np.random.default_rng(5)
+    x = rng.gamma(0.3, size=(2 * 20, 40)).astype(np.float32)
+    x[3, 5] = np.inf
+    x[4, 6] = np.nan
+    x[5, :] = np.nan
+    x[6, 9] = -np.inf
+    x[7, 2] = np.nan
+    x[7, 30] = np.inf
+    x[25, 11] = np.inf
+    x[26, 12] = np.nan
+    s = torch.from_numpy(x).view(2, 20, 40)
+    kw = dict(text_length=256, force_text=True, mode=mode)
+    ref = torch_ref.coverage_mask(s, **kw)
+    tb = 2
+    vt = tb if mode == "video_residual" else None
+    got = ops.coverage_mask(s.cuda(), 0.85, True, tb, tb, vt)
+    assert torch.equal(got.cpu(), ref)
