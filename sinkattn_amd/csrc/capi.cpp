@@ -468,7 +468,7 @@ int sinkattn_mean_pool_scores(const void* q, const void* k, int dtype, int64_t B
 
 size_t sinkattn_coverage_mask_workspace_bytes(int64_t H, int64_t nq) {
   const int64_t rows = H * nq > 0 ? H * nq : 0;
-  return (size_t)(((rows * 4 + 255) / 256) * 256 + ((rows + 255) / 256) * 256);
+  return (size_t)(((rows + 255) / 256) * 256);
 }
 
 int sinkattn_coverage_mask(const float* scores, int64_t H, int64_t nq, int64_t nk, float coverage,
@@ -497,8 +497,7 @@ int sinkattn_coverage_mask(const float* scores, int64_t H, int64_t nq, int64_t n
   a.mask = mask;
   a.counts = counts;
   a.idx = idx;
-  a.ws_top1 = reinterpret_cast<int32_t*>(workspace);
-  a.ws_flags = reinterpret_cast<uint8_t*>(workspace) + ((H * nq * 4 + 255) / 256) * 256;
+  a.ws_flags = reinterpret_cast<uint8_t*>(workspace);
   return hip_status(sa::launch_coverage_mask(a, (hipStream_t)stream), "coverage_mask launch");
 }
 

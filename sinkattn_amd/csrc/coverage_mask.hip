@@ -398,18 +398,24 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
 }
 
 // Value of lane `lane ^ M` (M = 1, 2, 4, 8: DPP; 16: ds_bpermute; 32: v_permlane32_swap).
+// Every lane has a source under these controls, so plain DPP moves suffice.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
+}
+
 template <int M>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v, int lane) {
   if constexpr (M == 1) {
-    return dpp_u32<0xb1, 0xf>(v, v);  // quad_perm [1,0,3,2]
+    return dpp_mov<0xb1>(v);  // quad_perm [1,0,3,2]
   } else if constexpr (M == 2) {
-    return dpp_u32<0x4e, 0xf>(v, v);  // quad_perm [2,3,0,1]
+    return dpp_mov<0x4e>(v);  // quad_perm [2,3,0,1]
   } else if constexpr (M == 4) {
-    const uint32_t up = dpp_u32<0x12c, 0xf>(v, v);    // row_ror:12 -> lane + 4 (mod 16)
-    const uint32_t down = dpp_u32<0x124, 0xf>(v, v);  // row_ror:4  -> lane - 4 (mod 16)
+    const uint32_t up = dpp_mov<0x12c>(v);    // row_ror:12 -> lane + 4 (mod 16)
+    const uint32_t down = dpp_mov<0x124>(v);  // row_ror:4  -> lane - 4 (mod 16)
     return (lane & 4) ? down : up;
   } else if constexpr (M == 8) {
-    return dpp_u32<0x128, 0xf>(v, v);  // row_ror:8 -> lane ^ 8
+    return dpp_mov<0x128>(v);  // row_ror:8 -> lane ^ 8
   } else if constexpr (M == 16) {
     return (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ 16) << 2, (int)v);
   } else {
@@ -427,29 +433,36 @@ __device__ __forceinline__ uint32_t order_key(float x) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+__device__ __forceinline__ uint32_t order_key_inverse(uint32_t k) {
+  if (k == 0xffffffffu) return 0x7fc00000u;  // NaN
+  return (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+}
+
 __device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src_lane_x4) {
   const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane_x4, (int)(uint32_t)v);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane_x4, (int)(uint32_t)(v >> 32));
   return ((uint64_t)hi << 32) | lo;
 }
 
-// Descending bitonic sort of 256*C distinct 64-bit keys held in registers: key (c, r) of
+// Descending bitonic sort of 256*C 32-bit order keys held in registers: key (c, r) of
 // lane l is element j = c*256 + l*4 + r.  Distances 1 and 2 stay inside a lane, 4..128
-// cross lanes (ds_bpermute), 256 and up cross a lane's own chunks.  A compare-exchange
-// leaves the larger key at the lower index inside blocks whose `size` bit of j is clear
-// and the smaller one where it is set, so the full network ends in descending order.
+// cross lanes, 256 and up cross a lane's own chunks.  A compare-exchange leaves the larger
+// key at the lower index inside blocks whose `size` bit of j is clear and the smaller one
+// where it is set, so the full network ends in descending order.  Only values are sorted:
+// which of several equal keys lands where is never read (rows whose selection depends on
+// the order of ties take the exact std::sort path).
 template <int C, int D>
-__device__ __forceinline__ void chunk_stage(uint64_t (&kk)[C][4], int size) {
+__device__ __forceinline__ void chunk_stage(uint32_t (&kk)[C][4], int size) {
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     if ((c & D) == 0) {
       const bool desc = ((c << 8) & size) == 0;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const uint64_t x = kk[c][r], y = kk[c | D][r];
-        const bool sw = (x < y) == desc;
-        kk[c][r] = sw ? y : x;
-        kk[c | D][r] = sw ? x : y;
+        const uint32_t x = kk[c][r], y = kk[c | D][r];
+        const uint32_t hi = max(x, y), lo = min(x, y);
+        kk[c][r] = desc ? hi : lo;
+        kk[c | D][r] = desc ? lo : hi;
       }
     }
   }
@@ -457,7 +470,7 @@ __device__ __forceinline__ void chunk_stage(uint64_t (&kk)[C][4], int size) {
 
 // Distances 4..128: lane l pairs with lane l ^ M (M = distance / 4).
 template <int C, int M>
-__device__ __forceinline__ void xlane_stage(uint64_t (&kk)[C][4], int size, int lane) {
+__device__ __forceinline__ void xlane_stage(uint32_t (&kk)[C][4], int size, int lane) {
   const bool lo = (lane & M) == 0;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
@@ -465,35 +478,33 @@ __device__ __forceinline__ void xlane_stage(uint64_t (&kk)[C][4], int size, int 
     const bool want_max = lo == desc;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const uint64_t x = kk[c][r];
-      const uint64_t y = ((uint64_t)xor_lane<M>((uint32_t)(x >> 32), lane) << 32) |
-                         xor_lane<M>((uint32_t)x, lane);
-      const bool take_y = want_max ? (y > x) : (y < x);
-      kk[c][r] = take_y ? y : x;
+      const uint32_t x = kk[c][r];
+      const uint32_t y = xor_lane<M>(x, lane);
+      kk[c][r] = want_max ? max(x, y) : min(x, y);
     }
   }
 }
 
 // Distances 1 and 2: pairs inside a lane.
 template <int C, int S>
-__device__ __forceinline__ void lane_stage(uint64_t (&kk)[C][4], int size, int lane) {
+__device__ __forceinline__ void lane_stage(uint32_t (&kk)[C][4], int size, int lane) {
 #pragma unroll
   for (int c = 0; c < C; ++c) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       if ((r & S) == 0) {
         const bool desc = ((((c << 8) | (lane << 2) | r)) & size) == 0;
-        const uint64_t x = kk[c][r], y = kk[c][r | S];
-        const bool sw = (x < y) == desc;
-        kk[c][r] = sw ? y : x;
-        kk[c][r | S] = sw ? x : y;
+        const uint32_t x = kk[c][r], y = kk[c][r | S];
+        const uint32_t hi = max(x, y), lo = min(x, y);
+        kk[c][r] = desc ? hi : lo;
+        kk[c][r | S] = desc ? lo : hi;
       }
     }
   }
 }
 
 template <int C>
-__device__ __forceinline__ void bitonic_sort_regs(uint64_t (&kk)[C][4], int lane) {
+__device__ __forceinline__ void bitonic_sort_regs(uint32_t (&kk)[C][4], int lane) {
   constexpr int P = 256 * C;
   for (int size = 2; size <= P; size <<= 1) {
     // Distances of 256 and up, longest first, each chunk distance a compile-time constant
@@ -539,9 +550,9 @@ template <int C>
 __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
   constexpr int NMAX = 256 * C;
   __shared__ float row[NMAX];
-  __shared__ unsigned long long keys[NMAX];
+  __shared__ uint32_t keys[NMAX];                          // sorted order keys
   __shared__ __attribute__((aligned(16))) float sv[NMAX];  // sorted values (tie-exact order when needed)
-  __shared__ int si[NMAX];                                // sorted indices
+  __shared__ int si[NMAX];                                // sorted indices (tie-exact rows only)
   __shared__ uint8_t m[NMAX];
   __shared__ int k_sh, exact_sh;
 
@@ -617,19 +628,17 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
       float res = tgt - sum_req;
       target = (res < 0.f) ? 0.f : res;
     }
-    // Candidate keys (value desc, index asc); positions past n hold 0, below every key.
-    uint64_t kk[C][4];
+    // Candidate order keys; positions past n hold 0, below every value's key.
+    uint32_t kk[C][4];
 #pragma unroll
     for (int c = 0; c < C; ++c)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = c * 256 + lane * 4 + r;
-        uint64_t key = 0ull;
+        uint32_t key = 0u;
         if (j < n) {
-          const float x = row[off + j];
           const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
-          const float cv = req ? neg_inf() : x;
-          key = ((uint64_t)order_key(cv) << 32) | (uint64_t)(~(uint32_t)j);
+          key = order_key(req ? neg_inf() : row[off + j]);
         }
         kk[c][r] = key;
       }
@@ -640,12 +649,9 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int j = c * 256 + lane * 4 + r;
         keys[j] = kk[c][r];
-        if (j < n) {
-          const int id = (int)(~(uint32_t)(kk[c][r] & 0xffffffffull));
-          si[j] = id;
-          const bool req = !video && ((qb < a.req_q) || (id < a.req_k));
-          sv[j] = req ? neg_inf() : row[off + id];
-        }
+        // The sorted value: -0 comes back as +0 and NaN as one NaN, neither of which
+        // changes a prefix sum or its comparison with the target.
+        if (j < n) sv[j] = __uint_as_float(order_key_inverse(kk[c][r]));
       }
     __syncthreads();
 
@@ -722,7 +728,7 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
       int k = target > 1e-6f ? (first >= 0 ? first + 1 : ncand) : 0;
       k = min(max(k, 0), n);
       int ex = 0;
-      if (k > 0 && k < n && (keys[k - 1] >> 32) == (keys[k] >> 32)) ex = 1;
+      if (k > 0 && k < n && keys[k - 1] == keys[k]) ex = 1;
       k_sh = k;
       exact_sh = ex;
     }
@@ -745,38 +751,33 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
     __syncthreads();
   }
 
-  for (int i = lane; i < k; i += 64) m[off + si[i]] = 1;
+  if (exact) {
+    for (int i = lane; i < k; i += 64) m[off + si[i]] = 1;
+  } else if (k > 0) {
+    // No tie straddles the cut: the first k of the sorted order are exactly the
+    // candidates whose key is at least the k-th largest key.
+    const uint32_t cut = keys[k - 1];
+    for (int j = lane; j < n; j += 64) {
+      const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
+      if (order_key(req ? neg_inf() : row[off + j]) >= cut) m[off + j] = 1;
+    }
+  }
   __syncthreads();
   if (!video && a.keep_diagonal && lane == 0 && qb < min(a.nq, nk)) m[qb] = 1;
   __syncthreads();
 
   // Row state for the empty-row fallback (applied by coverage_fixup_kernel once every
-  // row is known): empty flag, top-1 index, and whether that index still depends on the
-  // order of a tie at the top of the sort.
+  // row is known): the empty flag, and whether the row's top-1 index depends on the order
+  // of a tie at the top of the sort.
   int any = 0;
   for (int j = lane; j < nk; j += 64) any |= m[j];
   any = __any(any);
   uint8_t* mrow = a.mask + (int64_t)rid * nk;
   for (int j = lane; j < nk; j += 64) mrow[j] = m[j];
-  int top1 = 0, tie = 0;
-  if (video) {
-    // scores.argmax(dim=-1): the first NaN if there is one, else the first maximum
-    // (-0 == +0) -- the largest (order_key(x), ~j) over the full row.
-    uint64_t best = 0ull;
-    for (int j = lane; j < nk; j += 64) {
-      const uint64_t key = ((uint64_t)order_key(row[j]) << 32) | (uint64_t)(~(uint32_t)j);
-      best = key > best ? key : best;
-    }
-    best = wave_max_u64(best);
-    top1 = (int)(~(uint32_t)(best & 0xffffffffull));
-  } else if (lane == 0) {  // sorted_indices[..., 0]
-    top1 = si[0];
-    tie = (!exact && n > 1 && (keys[0] >> 32) == (keys[1] >> 32)) ? 1 : 0;
-  }
-  if (lane == 0) {
-    a.ws_top1[rid] = top1;
-    a.ws_flags[rid] = (uint8_t)((any ? 0 : 1) | (tie << 1));
-  }
+  // Joint rows whose top two keys are equal: their top-1 index depends on the order of
+  // that tie, so the fallback takes it from the exact std::sort order.
+  const int tie = (!video && n > 1 && keys[0] == keys[1]) ? 1 : 0;
+  if (lane == 0) a.ws_flags[rid] = (uint8_t)((any ? 0 : 1) | (tie << 1));
 }
 
 // Phase 2, one 64-thread work-group per row.  The reference's fallback
@@ -822,11 +823,16 @@ __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
   for (int j = lane; j < nk; j += 64) m[j] = mrow[j];
   __syncthreads();
   if (fallback) {
+    // Top-1: video -> scores.argmax(dim=-1) over the full row, the first NaN if there is
+    // one, else the first maximum (-0 == +0); joint -> sorted_indices[..., 0], the
+    // candidate of the largest key, from the exact std::sort order when the top two keys
+    // tie.  Without such a tie both are the largest (order_key, ~index) pair of the row.
     const uint8_t flags = a.ws_flags[rid];
-    if (lane == 0) {
-      int t = a.ws_top1[rid];
-      if (flags & 2) {  // joint branch, tie at the top: exact std::sort order
-        const float* src = a.scores + (int64_t)rid * nk;
+    const float* src = a.scores + (int64_t)rid * nk;
+    const bool video = a.mode == 1;
+    int t;
+    if (flags & 2) {
+      if (lane == 0) {
         for (int j = 0; j < nk; ++j) {
           const bool req = (qb < a.req_q) || (j < a.req_k);
           sv[j] = req ? neg_inf() : src[j];
@@ -834,8 +840,20 @@ __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
         }
         PairArr p{sv, si};
         std_sort(p, nk);
-        t = si[0];
       }
+      __syncthreads();
+      t = si[0];
+    } else {
+      uint64_t best = 0ull;
+      for (int j = lane; j < nk; j += 64) {
+        const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
+        const uint64_t key = ((uint64_t)order_key(req ? neg_inf() : src[j]) << 32) | (uint64_t)(~(uint32_t)j);
+        best = key > best ? key : best;
+      }
+      best = wave_max_u64(best);
+      t = (int)(~(uint32_t)(best & 0xffffffffull));
+    }
+    if (lane == 0) {
       m[t] = flags & 1;
       mrow[t] = flags & 1;
     }

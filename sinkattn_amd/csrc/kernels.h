@@ -60,8 +60,7 @@ struct MaskArgs {
   uint8_t* mask;
   int32_t* counts;
   int32_t* idx;
-  int32_t* ws_top1;   // [H*nq] workspace
-  uint8_t* ws_flags;  // [H*nq] workspace
+  uint8_t* ws_flags;  // [H*nq] workspace (empty-row and top-tie flags), padded to 256 B
 };
 
 // Token mean pooling: rows [0, prefix) copied, then groups of `gap` rows averaged

@@ -102,6 +102,26 @@ def test_empty_row_fallback_quirk_on_gpu(oracle_lib):
     assert torch.equal(torch.from_numpy(oracle_lib.coverage_mask(s.numpy(), 0.85, False)), ref)
 
 
+@pytest.mark.parametrize("nk,force_text", [(300, False), (700, True)])
+def test_empty_row_fallback_many_rows(oracle_lib, nk, force_text):
+    # zero rows without the diagonal come out empty, so every row's top-1 bit is rewritten:
+    # unique maxima, ties at the top, and required text blocks (-inf candidates) included
+    rng = np.random.default_rng(nk)
+    x = rng.gamma(0.3, size=(2 * 24, nk)).astype(np.float32)
+    x[5] = 0.0
+    x[30] = 0.0
+    x[7, :3] = x[7].max() + 1.0  # tie at the top
+    s = torch.from_numpy(x).view(2, 24, nk)
+    kw = dict(keep_diagonal=False, text_length=256 if force_text else 0, force_text=force_text)
+    ref = torch_ref.coverage_mask(s, **kw)
+    rq = rk = 2 if force_text else 0
+    got, counts, idx = ops.coverage_mask(s.cuda(), 0.85, False, rq, rk, None, want_lists=True)
+    assert torch.equal(got.cpu(), ref)
+    _check_lists(got, counts, idx)
+    if not force_text:
+        assert np.array_equal(oracle_lib.coverage_mask(s.numpy(), 0.85, False), ref.numpy())
+
+
 def test_many_tie_rows_exact_permutation(oracle_lib):
     # small-integer scores: ties straddle the cut in most rows
     rng = np.random.default_rng(0)
