@@ -134,89 +134,98 @@ __device__ float aten_row_sum(const RowView& r) {
 }
 
 // --- libstdc++ std::sort emulation on (value, index) pairs, descending comparator -----
-struct PairArr {
-  float* v;
-  int* id;
-  __device__ __forceinline__ bool comp(int a, int b) const {  // element a before b
-    const float x = v[a], y = v[b];
-    return (__builtin_isnan(x) && !__builtin_isnan(y)) || (x > y);
-  }
-  __device__ __forceinline__ bool comp_val(float x, int b) const {
-    const float y = v[b];
-    return (__builtin_isnan(x) && !__builtin_isnan(y)) || (x > y);
-  }
-  __device__ __forceinline__ bool comp_val2(int a, float y) const {
-    const float x = v[a];
-    return (__builtin_isnan(x) && !__builtin_isnan(y)) || (x > y);
-  }
-  __device__ __forceinline__ void swap(int a, int b) const {
-    const float tv = v[a]; v[a] = v[b]; v[b] = tv;
-    const int ti = id[a]; id[a] = id[b]; id[b] = ti;
-  }
-};
-
-__device__ void std_move_median_to_first(const PairArr& p, int result, int a, int b, int c) {
-  if (p.comp(a, b)) {
-    if (p.comp(b, c)) p.swap(result, b);
-    else if (p.comp(a, c)) p.swap(result, c);
-    else p.swap(result, a);
-  } else if (p.comp(a, c)) {
-    p.swap(result, a);
-  } else if (p.comp(b, c)) {
-    p.swap(result, c);
-  } else {
-    p.swap(result, b);
-  }
+// An entry packs the value's bits (low word) and its index (high word), so a move is one
+// 64-bit LDS access.  `e` points one entry into an array of n + 2 entries: the scans read
+// one entry ahead (e[-1] .. e[n]), always inside the array, and a value read ahead is
+// only compared once the original algorithm reaches its position.
+__device__ __forceinline__ float pval(uint64_t x) { return __uint_as_float((uint32_t)x); }
+__device__ __forceinline__ int pidx(uint64_t x) { return (int)(x >> 32); }
+__device__ __forceinline__ uint64_t pmake(float v, int i) {
+  return ((uint64_t)(uint32_t)i << 32) | __float_as_uint(v);
+}
+// The comparator: x goes before y.
+__device__ __forceinline__ bool pcomp(float x, float y) {
+  return (__builtin_isnan(x) && !__builtin_isnan(y)) || (x > y);
 }
 
-__device__ int std_unguarded_partition(const PairArr& p, int first, int last, int pivot) {
+__device__ void std_move_median_to_first(uint64_t* e, int result, int a, int b, int c) {
+  const uint64_t ea = e[a], eb = e[b], ec = e[c];
+  const float va = pval(ea), vb = pval(eb), vc = pval(ec);
+  int pick;
+  uint64_t ep;
+  if (pcomp(va, vb)) {
+    if (pcomp(vb, vc)) { pick = b; ep = eb; }
+    else if (pcomp(va, vc)) { pick = c; ep = ec; }
+    else { pick = a; ep = ea; }
+  } else if (pcomp(va, vc)) {
+    pick = a; ep = ea;
+  } else if (pcomp(vb, vc)) {
+    pick = c; ep = ec;
+  } else {
+    pick = b; ep = eb;
+  }
+  const uint64_t er = e[result];
+  e[result] = ep;
+  e[pick] = er;
+}
+
+// The pivot (at `pivot`, just before the range) is never moved by the partition, so its
+// value stays in a register.
+__device__ int std_unguarded_partition(uint64_t* e, int first, int last, int pivot) {
+  const float pv = pval(e[pivot]);
   while (true) {
-    while (p.comp(first, pivot)) ++first;
+    uint64_t ef = e[first], ef1 = e[first + 1];
+    while (pcomp(pval(ef), pv)) {
+      ++first;
+      ef = ef1;
+      ef1 = e[first + 1];
+    }
     --last;
-    while (p.comp(pivot, last)) --last;
+    uint64_t el = e[last], el1 = e[last - 1];
+    while (pcomp(pv, pval(el))) {
+      --last;
+      el = el1;
+      el1 = e[last - 1];
+    }
     if (!(first < last)) return first;
-    p.swap(first, last);
+    e[first] = el;
+    e[last] = ef;
     ++first;
   }
 }
 
 // __adjust_heap(first, hole, len, value) on [base, base+len)
-__device__ void std_adjust_heap(const PairArr& p, int base, int hole, int len, float val, int vid) {
+__device__ void std_adjust_heap(uint64_t* e, int base, int hole, int len, uint64_t val) {
   const int top = hole;
   int second = hole;
   while (second < (len - 1) / 2) {
     second = 2 * (second + 1);
-    if (p.comp(base + second, base + second - 1)) second--;
-    p.v[base + hole] = p.v[base + second];
-    p.id[base + hole] = p.id[base + second];
+    if (pcomp(pval(e[base + second]), pval(e[base + second - 1]))) second--;
+    e[base + hole] = e[base + second];
     hole = second;
   }
   if ((len & 1) == 0 && second == (len - 2) / 2) {
     second = 2 * (second + 1);
-    p.v[base + hole] = p.v[base + second - 1];
-    p.id[base + hole] = p.id[base + second - 1];
+    e[base + hole] = e[base + second - 1];
     hole = second - 1;
   }
   // __push_heap
+  const float vv = pval(val);
   int parent = (hole - 1) / 2;
-  while (hole > top && p.comp_val2(base + parent, val)) {
-    p.v[base + hole] = p.v[base + parent];
-    p.id[base + hole] = p.id[base + parent];
+  while (hole > top && pcomp(pval(e[base + parent]), vv)) {
+    e[base + hole] = e[base + parent];
     hole = parent;
     parent = (hole - 1) / 2;
   }
-  p.v[base + hole] = val;
-  p.id[base + hole] = vid;
+  e[base + hole] = val;
 }
 
-__device__ void std_heap_sort(const PairArr& p, int first, int last) {
+__device__ void std_heap_sort(uint64_t* e, int first, int last) {
   const int len = last - first;
   if (len >= 2) {  // __make_heap
     int parent = (len - 2) / 2;
     while (true) {
-      const float val = p.v[first + parent];
-      const int vid = p.id[first + parent];
-      std_adjust_heap(p, first, parent, len, val, vid);
+      std_adjust_heap(e, first, parent, len, e[first + parent]);
       if (parent == 0) break;
       parent--;
     }
@@ -224,51 +233,49 @@ __device__ void std_heap_sort(const PairArr& p, int first, int last) {
   // __sort_heap
   while (last - first > 1) {
     --last;
-    const float val = p.v[last];
-    const int vid = p.id[last];
-    p.v[last] = p.v[first];
-    p.id[last] = p.id[first];
-    std_adjust_heap(p, first, 0, last - first, val, vid);
+    const uint64_t val = e[last];
+    e[last] = e[first];
+    std_adjust_heap(e, first, 0, last - first, val);
   }
 }
 
-__device__ void std_unguarded_linear_insert(const PairArr& p, int last) {
-  const float val = p.v[last];
-  const int vid = p.id[last];
+__device__ void std_unguarded_linear_insert(uint64_t* e, int last) {
+  const uint64_t val = e[last];
+  const float vv = pval(val);
   int next = last - 1;
-  while (p.comp_val(val, next)) {
-    p.v[last] = p.v[next];
-    p.id[last] = p.id[next];
+  uint64_t en = e[next], en1 = e[next - 1];
+  while (pcomp(vv, pval(en))) {
+    e[last] = en;
     last = next;
     --next;
+    en = en1;
+    en1 = e[next - 1];
   }
-  p.v[last] = val;
-  p.id[last] = vid;
+  e[last] = val;
 }
 
-__device__ void std_insertion_sort(const PairArr& p, int first, int last) {
+__device__ void std_insertion_sort(uint64_t* e, int first, int last) {
   if (first == last) return;
   for (int i = first + 1; i != last; ++i) {
-    if (p.comp(i, first)) {
-      const float val = p.v[i];
-      const int vid = p.id[i];
-      for (int j = i; j > first; --j) {
-        p.v[j] = p.v[j - 1];
-        p.id[j] = p.id[j - 1];
-      }
-      p.v[first] = val;
-      p.id[first] = vid;
+    const uint64_t ei = e[i];
+    if (pcomp(pval(ei), pval(e[first]))) {
+      for (int j = i; j > first; --j) e[j] = e[j - 1];
+      e[first] = ei;
     } else {
-      std_unguarded_linear_insert(p, i);
+      std_unguarded_linear_insert(e, i);
     }
   }
 }
 
-__device__ void std_sort(const PairArr& p, int n) {
+// `stk` is a 3 x 64-entry LDS stack for the pending ranges (a private array would live in
+// scratch memory); at most 2*log2(n) + 1 ranges are pending at once.
+__device__ void std_sort(uint64_t* e, int n, int* stk) {
   if (n <= 1) return;
   constexpr int kThreshold = 16;
   // __introsort_loop with an explicit stack: [first, last, depth]
-  int st_first[64], st_last[64], st_depth[64];
+  int* st_first = stk;
+  int* st_last = stk + 64;
+  int* st_depth = stk + 128;
   int sp = 0;
   st_first[sp] = 0; st_last[sp] = n; st_depth[sp] = 2 * (31 - __clz(n)); ++sp;
   while (sp > 0) {
@@ -276,23 +283,23 @@ __device__ void std_sort(const PairArr& p, int n) {
     int first = st_first[sp], last = st_last[sp], depth = st_depth[sp];
     while (last - first > kThreshold) {
       if (depth == 0) {
-        std_heap_sort(p, first, last);
+        std_heap_sort(e, first, last);
         break;
       }
       --depth;
       const int mid = first + (last - first) / 2;
-      std_move_median_to_first(p, first, first + 1, mid, last - 1);
-      const int cut = std_unguarded_partition(p, first + 1, last, first);
+      std_move_median_to_first(e, first, first + 1, mid, last - 1);
+      const int cut = std_unguarded_partition(e, first + 1, last, first);
       st_first[sp] = cut; st_last[sp] = last; st_depth[sp] = depth; ++sp;
       last = cut;
     }
   }
   // __final_insertion_sort
   if (n > kThreshold) {
-    std_insertion_sort(p, 0, kThreshold);
-    for (int i = kThreshold; i < n; ++i) std_unguarded_linear_insert(p, i);
+    std_insertion_sort(e, 0, kThreshold);
+    for (int i = kThreshold; i < n; ++i) std_unguarded_linear_insert(e, i);
   } else {
-    std_insertion_sort(p, 0, n);
+    std_insertion_sort(e, 0, n);
   }
 }
 
@@ -551,8 +558,9 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
   constexpr int NMAX = 256 * C;
   __shared__ float row[NMAX];
   __shared__ uint32_t keys[NMAX];                          // sorted order keys
-  __shared__ __attribute__((aligned(16))) float sv[NMAX];  // sorted values (tie-exact order when needed)
-  __shared__ int si[NMAX];                                // sorted indices (tie-exact rows only)
+  __shared__ __attribute__((aligned(16))) float sv[NMAX];  // sorted values
+  __shared__ uint64_t pe[NMAX + 2];  // (value, index) entries in std::sort order, tie-exact rows
+  __shared__ int stk[3 * 64];
   __shared__ uint8_t m[NMAX];
   __shared__ int k_sh, exact_sh;
 
@@ -740,19 +748,18 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
   // Exact permutation for rows whose selection depends on the order of tied values.
   if (do_select && exact) {
     if (lane == 0) {
+      uint64_t* e = pe + 1;
       for (int j = 0; j < n; ++j) {
         const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
-        sv[j] = req ? neg_inf() : row[off + j];
-        si[j] = j;
+        e[j] = pmake(req ? neg_inf() : row[off + j], j);
       }
-      PairArr p{sv, si};
-      std_sort(p, n);
+      std_sort(e, n, stk);
     }
     __syncthreads();
   }
 
   if (exact) {
-    for (int i = lane; i < k; i += 64) m[off + si[i]] = 1;
+    for (int i = lane; i < k; i += 64) m[off + pidx(pe[1 + i])] = 1;
   } else if (k > 0) {
     // No tie straddles the cut: the first k of the sorted order are exactly the
     // candidates whose key is at least the k-th largest key.
@@ -788,8 +795,8 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
 template <int C>
 __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
   constexpr int NMAX = 256 * C;
-  __shared__ float sv[NMAX];
-  __shared__ int si[NMAX];
+  __shared__ uint64_t pe[NMAX + 2];
+  __shared__ int stk[3 * 64];
   __shared__ uint8_t m[NMAX];
   const int lane = threadIdx.x;
   const int rid = blockIdx.x;
@@ -833,16 +840,15 @@ __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
     int t;
     if (flags & 2) {
       if (lane == 0) {
+        uint64_t* e = pe + 1;
         for (int j = 0; j < nk; ++j) {
           const bool req = (qb < a.req_q) || (j < a.req_k);
-          sv[j] = req ? neg_inf() : src[j];
-          si[j] = j;
+          e[j] = pmake(req ? neg_inf() : src[j], j);
         }
-        PairArr p{sv, si};
-        std_sort(p, nk);
+        std_sort(e, nk, stk);
       }
       __syncthreads();
-      t = si[0];
+      t = pidx(pe[1]);
     } else {
       uint64_t best = 0ull;
       for (int j = lane; j < nk; j += 64) {
