@@ -267,12 +267,18 @@ __device__ void std_insertion_sort(uint64_t* e, int first, int last) {
   }
 }
 
-// `stk` is a 3 x 64-entry LDS stack for the pending ranges (a private array would live in
-// scratch memory); at most 2*log2(n) + 1 ranges are pending at once.
-__device__ void std_sort(uint64_t* e, int n, int* stk) {
-  if (n <= 1) return;
+// libstdc++'s std::sort(e, e + n) as far as positions [p0, p1) are concerned: after the
+// call those positions hold exactly what the full sort puts there.  Introsort's
+// sub-ranges are sorted independently of each other, and its final insertion pass never
+// moves an element across the boundary of a sub-range left by the partitions (the
+// elements before a boundary are never strictly after those behind it), so it acts as an
+// insertion sort of each such range.  The walk therefore follows only partitions whose
+// range meets [p0, p1) and insertion-sorts only the leftover ranges it reaches; with
+// [0, n) it is the full sort.  `stk` is a 3 x 64-entry LDS stack of pending ranges (at
+// most 2*log2(n) + 1 at once).
+__device__ void std_sort_positions(uint64_t* e, int n, int p0, int p1, int* stk) {
+  if (n <= 1 || p0 >= p1) return;
   constexpr int kThreshold = 16;
-  // __introsort_loop with an explicit stack: [first, last, depth]
   int* st_first = stk;
   int* st_last = stk + 64;
   int* st_depth = stk + 128;
@@ -281,25 +287,32 @@ __device__ void std_sort(uint64_t* e, int n, int* stk) {
   while (sp > 0) {
     --sp;
     int first = st_first[sp], last = st_last[sp], depth = st_depth[sp];
+    bool heap_sorted = false;
+    // __introsort_loop on [first, last), keeping to the parts that meet [p0, p1)
     while (last - first > kThreshold) {
       if (depth == 0) {
         std_heap_sort(e, first, last);
+        heap_sorted = true;
         break;
       }
       --depth;
       const int mid = first + (last - first) / 2;
       std_move_median_to_first(e, first, first + 1, mid, last - 1);
       const int cut = std_unguarded_partition(e, first + 1, last, first);
-      st_first[sp] = cut; st_last[sp] = last; st_depth[sp] = depth; ++sp;
-      last = cut;
+      const bool left = first < p1 && cut > p0;
+      const bool right = cut < p1 && last > p0;
+      if (left && right) {
+        st_first[sp] = cut; st_last[sp] = last; st_depth[sp] = depth; ++sp;
+        last = cut;
+      } else if (right) {
+        first = cut;
+      } else {
+        last = cut;
+      }
     }
-  }
-  // __final_insertion_sort
-  if (n > kThreshold) {
-    std_insertion_sort(e, 0, kThreshold);
-    for (int i = kThreshold; i < n; ++i) std_unguarded_linear_insert(e, i);
-  } else {
-    std_insertion_sort(e, 0, n);
+    // __final_insertion_sort restricted to this leftover range (a heap-sorted range is
+    // already in order and the insertion pass leaves it unchanged)
+    if (!heap_sorted) std_insertion_sort(e, first, last);
   }
 }
 
@@ -562,7 +575,7 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
   __shared__ uint64_t pe[NMAX + 2];  // (value, index) entries in std::sort order, tie-exact rows
   __shared__ int stk[3 * 64];
   __shared__ uint8_t m[NMAX];
-  __shared__ int k_sh, exact_sh;
+  __shared__ int k_sh, exact_sh, p0_sh;
 
   const int lane = threadIdx.x;
   const int rid = blockIdx.x;  // h * nq + qb
@@ -745,21 +758,46 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
   }
 
   const int k = do_select ? k_sh : 0;
-  // Exact permutation for rows whose selection depends on the order of tied values.
+  // Rows whose selection depends on the order of tied values: the tie group at the cut
+  // occupies sorted positions [p0, p1) (keys equal to the k-th key), and std::sort's
+  // order of exactly those positions decides which of its members are among the first k.
   if (do_select && exact) {
     if (lane == 0) {
+      const uint32_t t = keys[k - 1];
+      int p0 = k - 1, p1 = k + 1;  // keys[k - 1] == keys[k] == t
+      {
+        int lo = 0, hi = k - 1;  // first index whose key is not above t
+        while (lo < hi) {
+          const int md = (lo + hi) >> 1;
+          if (keys[md] > t) lo = md + 1; else hi = md;
+        }
+        p0 = lo;
+        lo = k + 1; hi = n;  // first index whose key is below t
+        while (lo < hi) {
+          const int md = (lo + hi) >> 1;
+          if (keys[md] >= t) lo = md + 1; else hi = md;
+        }
+        p1 = lo;
+      }
       uint64_t* e = pe + 1;
       for (int j = 0; j < n; ++j) {
         const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
         e[j] = pmake(req ? neg_inf() : row[off + j], j);
       }
-      std_sort(e, n, stk);
+      std_sort_positions(e, n, p0, p1, stk);
+      p0_sh = p0;
     }
     __syncthreads();
   }
 
   if (exact) {
-    for (int i = lane; i < k; i += 64) m[off + pidx(pe[1 + i])] = 1;
+    // keys above the tie, then the tie group's members in std::sort order up to the cut
+    const uint32_t t = keys[k - 1];
+    for (int j = lane; j < n; j += 64) {
+      const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
+      if (order_key(req ? neg_inf() : row[off + j]) > t) m[off + j] = 1;
+    }
+    for (int i = p0_sh + lane; i < k; i += 64) m[off + pidx(pe[1 + i])] = 1;
   } else if (k > 0) {
     // No tie straddles the cut: the first k of the sorted order are exactly the
     // candidates whose key is at least the k-th largest key.
@@ -845,7 +883,7 @@ __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
           const bool req = (qb < a.req_q) || (j < a.req_k);
           e[j] = pmake(req ? neg_inf() : src[j], j);
         }
-        std_sort(e, nk, stk);
+        std_sort_positions(e, nk, 0, 1, stk);
       }
       __syncthreads();
       t = pidx(pe[1]);
