@@ -169,31 +169,6 @@ __device__ void std_move_median_to_first(uint64_t* e, int result, int a, int b, 
   e[pick] = er;
 }
 
-// The pivot (at `pivot`, just before the range) is never moved by the partition, so its
-// value stays in a register.
-__device__ int std_unguarded_partition(uint64_t* e, int first, int last, int pivot) {
-  const float pv = pval(e[pivot]);
-  while (true) {
-    uint64_t ef = e[first], ef1 = e[first + 1];
-    while (pcomp(pval(ef), pv)) {
-      ++first;
-      ef = ef1;
-      ef1 = e[first + 1];
-    }
-    --last;
-    uint64_t el = e[last], el1 = e[last - 1];
-    while (pcomp(pv, pval(el))) {
-      --last;
-      el = el1;
-      el1 = e[last - 1];
-    }
-    if (!(first < last)) return first;
-    e[first] = el;
-    e[last] = ef;
-    ++first;
-  }
-}
-
 // __adjust_heap(first, hole, len, value) on [base, base+len)
 __device__ void std_adjust_heap(uint64_t* e, int base, int hole, int len, uint64_t val) {
   const int top = hole;
@@ -267,6 +242,57 @@ __device__ void std_insertion_sort(uint64_t* e, int first, int last) {
   }
 }
 
+// __unguarded_partition(e + first, e + last, e + pivot) computed by the whole wave, with
+// the serial scans' result.  Call a position an L-stop when its original value is not
+// before the pivot and an R-stop when it is not after it.  The k-th iteration of the
+// serial loop stops its left scan at the k-th L-stop l_k and its right scan at the k-th
+// R-stop from the right r_k, and swaps them while l_k < r_k: until the scans cross they
+// read only untouched positions.  With s such swaps, the next left scan stops at l_s or,
+// failing an untouched L-stop before it, at r_{s-1} (which now holds an L-stop's value):
+// the cut is min(l_s, r_{s-1}).  The 2s swapped positions are distinct.  `lp` and `rp`
+// receive the stop positions (last - first entries each).  All 64 lanes call it.
+__device__ int wave_unguarded_partition(uint64_t* e, int first, int last, int pivot, int* lp,
+                                        int* rp, int lane) {
+  const float pv = pval(e[pivot]);
+  const uint64_t below = (1ull << lane) - 1ull;
+  int nl = 0, nr = 0;
+  for (int c0 = first; c0 < last; c0 += 64) {
+    const int i = c0 + lane;       // ascending positions
+    const int j = last - 1 - (c0 - first) - lane;  // descending positions
+    const bool ini = i < last, inj = j >= first;
+    const float xi = ini ? pval(e[i]) : 0.f;
+    const float xj = inj ? pval(e[j]) : 0.f;
+    const bool isl = ini && !pcomp(xi, pv);
+    const bool isr = inj && !pcomp(pv, xj);
+    const uint64_t bl = __ballot(isl), br = __ballot(isr);
+    if (isl) lp[nl + __popcll(bl & below)] = i;
+    if (isr) rp[nr + __popcll(br & below)] = j;
+    nl += __popcll(bl);
+    nr += __popcll(br);
+  }
+  __syncthreads();
+  // l_k < r_k holds for a prefix of k; count it.
+  int sw = 0;
+  const int kmax = min(nl, nr);
+  for (int k0 = 0; k0 < kmax; k0 += 64) {
+    const int k = k0 + lane;
+    sw += __popcll(__ballot(k < kmax && lp[k] < rp[k]));
+  }
+  int cut = sw < nl ? lp[sw] : 0x7fffffff;
+  if (sw > 0) cut = min(cut, rp[sw - 1]);
+  for (int k0 = 0; k0 < sw; k0 += 64) {
+    const int k = k0 + lane;
+    if (k < sw) {
+      const int a = lp[k], b = rp[k];
+      const uint64_t ea = e[a], eb = e[b];
+      e[a] = eb;
+      e[b] = ea;
+    }
+  }
+  __syncthreads();
+  return cut;
+}
+
 // libstdc++'s std::sort(e, e + n) as far as positions [p0, p1) are concerned: after the
 // call those positions hold exactly what the full sort puts there.  Introsort's
 // sub-ranges are sorted independently of each other, and its final insertion pass never
@@ -276,9 +302,13 @@ __device__ void std_insertion_sort(uint64_t* e, int first, int last) {
 // range meets [p0, p1) and insertion-sorts only the leftover ranges it reaches; with
 // [0, n) it is the full sort.  `stk` is a 3 x 64-entry LDS stack of pending ranges (at
 // most 2*log2(n) + 1 at once).
-__device__ void std_sort_positions(uint64_t* e, int n, int p0, int p1, int* stk) {
+// Partitions are done by the whole wave; median selection, heap sort and the leftover
+// insertion sorts stay on lane 0.  `lp` and `rp` hold n entries each.  All 64 lanes call it.
+__device__ void wave_sort_positions(uint64_t* e, int n, int p0, int p1, int* stk, int* lp,
+                                    int* rp, int lane) {
   if (n <= 1 || p0 >= p1) return;
   constexpr int kThreshold = 16;
+  // The stack is written by every lane with the same values and read by all of them.
   int* st_first = stk;
   int* st_last = stk + 64;
   int* st_depth = stk + 128;
@@ -288,17 +318,17 @@ __device__ void std_sort_positions(uint64_t* e, int n, int p0, int p1, int* stk)
     --sp;
     int first = st_first[sp], last = st_last[sp], depth = st_depth[sp];
     bool heap_sorted = false;
-    // __introsort_loop on [first, last), keeping to the parts that meet [p0, p1)
     while (last - first > kThreshold) {
       if (depth == 0) {
-        std_heap_sort(e, first, last);
+        if (lane == 0) std_heap_sort(e, first, last);
         heap_sorted = true;
         break;
       }
       --depth;
       const int mid = first + (last - first) / 2;
-      std_move_median_to_first(e, first, first + 1, mid, last - 1);
-      const int cut = std_unguarded_partition(e, first + 1, last, first);
+      if (lane == 0) std_move_median_to_first(e, first, first + 1, mid, last - 1);
+      __syncthreads();
+      const int cut = wave_unguarded_partition(e, first + 1, last, first, lp, rp, lane);
       const bool left = first < p1 && cut > p0;
       const bool right = cut < p1 && last > p0;
       if (left && right) {
@@ -310,9 +340,8 @@ __device__ void std_sort_positions(uint64_t* e, int n, int p0, int p1, int* stk)
         last = cut;
       }
     }
-    // __final_insertion_sort restricted to this leftover range (a heap-sorted range is
-    // already in order and the insertion pass leaves it unchanged)
-    if (!heap_sorted) std_insertion_sort(e, first, last);
+    if (!heap_sorted && lane == 0) std_insertion_sort(e, first, last);
+    __syncthreads();
   }
 }
 
@@ -574,8 +603,9 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
   __shared__ __attribute__((aligned(16))) float sv[NMAX];  // sorted values
   __shared__ uint64_t pe[NMAX + 2];  // (value, index) entries in std::sort order, tie-exact rows
   __shared__ int stk[3 * 64];
+  __shared__ int lrp[2 * NMAX];  // partition stop positions, tie-exact rows
   __shared__ uint8_t m[NMAX];
-  __shared__ int k_sh, exact_sh, p0_sh;
+  __shared__ int k_sh, exact_sh, p0_sh, p1_sh;
 
   const int lane = threadIdx.x;
   const int rid = blockIdx.x;  // h * nq + qb
@@ -764,30 +794,26 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
   if (do_select && exact) {
     if (lane == 0) {
       const uint32_t t = keys[k - 1];
-      int p0 = k - 1, p1 = k + 1;  // keys[k - 1] == keys[k] == t
-      {
-        int lo = 0, hi = k - 1;  // first index whose key is not above t
-        while (lo < hi) {
-          const int md = (lo + hi) >> 1;
-          if (keys[md] > t) lo = md + 1; else hi = md;
-        }
-        p0 = lo;
-        lo = k + 1; hi = n;  // first index whose key is below t
-        while (lo < hi) {
-          const int md = (lo + hi) >> 1;
-          if (keys[md] >= t) lo = md + 1; else hi = md;
-        }
-        p1 = lo;
+      int lo = 0, hi = k - 1;  // first index whose key is not above t
+      while (lo < hi) {
+        const int md = (lo + hi) >> 1;
+        if (keys[md] > t) lo = md + 1; else hi = md;
       }
-      uint64_t* e = pe + 1;
-      for (int j = 0; j < n; ++j) {
-        const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
-        e[j] = pmake(req ? neg_inf() : row[off + j], j);
+      p0_sh = lo;
+      lo = k + 1; hi = n;  // first index whose key is below t (keys[k] == t)
+      while (lo < hi) {
+        const int md = (lo + hi) >> 1;
+        if (keys[md] >= t) lo = md + 1; else hi = md;
       }
-      std_sort_positions(e, n, p0, p1, stk);
-      p0_sh = p0;
+      p1_sh = lo;
+    }
+    uint64_t* e = pe + 1;
+    for (int j = lane; j < n; j += 64) {
+      const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
+      e[j] = pmake(req ? neg_inf() : row[off + j], j);
     }
     __syncthreads();
+    wave_sort_positions(e, n, p0_sh, p1_sh, stk, lrp, lrp + NMAX, lane);
   }
 
   if (exact) {
@@ -835,6 +861,7 @@ __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
   constexpr int NMAX = 256 * C;
   __shared__ uint64_t pe[NMAX + 2];
   __shared__ int stk[3 * 64];
+  __shared__ int lrp[2 * NMAX];
   __shared__ uint8_t m[NMAX];
   const int lane = threadIdx.x;
   const int rid = blockIdx.x;
@@ -877,15 +904,13 @@ __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
     const bool video = a.mode == 1;
     int t;
     if (flags & 2) {
-      if (lane == 0) {
-        uint64_t* e = pe + 1;
-        for (int j = 0; j < nk; ++j) {
-          const bool req = (qb < a.req_q) || (j < a.req_k);
-          e[j] = pmake(req ? neg_inf() : src[j], j);
-        }
-        std_sort_positions(e, nk, 0, 1, stk);
+      uint64_t* e = pe + 1;
+      for (int j = lane; j < nk; j += 64) {
+        const bool req = (qb < a.req_q) || (j < a.req_k);
+        e[j] = pmake(req ? neg_inf() : src[j], j);
       }
       __syncthreads();
+      wave_sort_positions(e, nk, 0, 1, stk, lrp, lrp + NMAX, lane);
       t = pidx(pe[1]);
     } else {
       uint64_t best = 0ull;
