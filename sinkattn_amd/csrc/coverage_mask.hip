@@ -33,6 +33,8 @@ namespace sa {
 // Row capacity: instances hold rows of 256 * C key blocks for C = 1, 2, 4, 8, 16 (5.3 KB
 // to 84 KB of LDS), so short rows keep many work-groups resident per CU.
 constexpr int kMaskMaxN = 4096;
+// Rows per work-group of the fixup pass.
+constexpr int kFixupRows = 16;
 
 // --- ATen-compatible fp32 row sum ---------------------------------------------------
 // x[i] * mul(i) is summed; mul is 1 (plain) or the 0/1 required flag (masked sum).
@@ -851,7 +853,7 @@ __global__ __launch_bounds__(64) void coverage_mask_kernel(MaskArgs a) {
   if (lane == 0) a.ws_flags[rid] = (uint8_t)((any ? 0 : 1) | (tie << 1));
 }
 
-// Phase 2, one 64-thread work-group per row.  The reference's fallback
+// Phase 2, one 64-thread work-group per kFixupRows rows.  The reference's fallback
 // `mask.scatter_(-1, top1, empty_rows.unsqueeze(-1))` (sparse_attention.py:327-330,
 // 371-374) runs when ANY row of the tensor is empty and then sets mask[r, top1[r]] =
 // empty[r] for EVERY row r -- it also clears the top-1 bit of non-empty rows.  Then the
@@ -864,9 +866,7 @@ __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
   __shared__ int lrp[2 * NMAX];
   __shared__ uint8_t m[NMAX];
   const int lane = threadIdx.x;
-  const int rid = blockIdx.x;
   const int rows = a.H * a.nq;
-  const int qb = rid % a.nq;
   const int nk = a.nk;
   // Empty flags (bit 0 of each byte), four rows per 32-bit word; the flag region is
   // padded to 256 bytes, and bytes past `rows` are masked off.
@@ -891,54 +891,61 @@ __global__ __launch_bounds__(64) void coverage_fixup_kernel(MaskArgs a) {
     }
   }
   const bool fallback = __any(any_empty != 0);
-  uint8_t* mrow = a.mask + (int64_t)rid * nk;
-  for (int j = lane; j < nk; j += 64) m[j] = mrow[j];
-  __syncthreads();
-  if (fallback) {
-    // Top-1: video -> scores.argmax(dim=-1) over the full row, the first NaN if there is
-    // one, else the first maximum (-0 == +0); joint -> sorted_indices[..., 0], the
-    // candidate of the largest key, from the exact std::sort order when the top two keys
-    // tie.  Without such a tie both are the largest (order_key, ~index) pair of the row.
-    const uint8_t flags = a.ws_flags[rid];
-    const float* src = a.scores + (int64_t)rid * nk;
-    const bool video = a.mode == 1;
-    int t;
-    if (flags & 2) {
-      uint64_t* e = pe + 1;
-      for (int j = lane; j < nk; j += 64) {
-        const bool req = (qb < a.req_q) || (j < a.req_k);
-        e[j] = pmake(req ? neg_inf() : src[j], j);
+  if (!fallback && a.idx == nullptr && a.counts == nullptr) return;  // the mask is final
+  // kFixupRows rows per work-group share the one scan of the flags above.
+  const int rid_end = (int)min((int64_t)rows, ((int64_t)blockIdx.x + 1) * kFixupRows);
+  for (int rid = (int)blockIdx.x * kFixupRows; rid < rid_end; ++rid) {
+    const int qb = rid % a.nq;
+    uint8_t* mrow = a.mask + (int64_t)rid * nk;
+    for (int j = lane; j < nk; j += 64) m[j] = mrow[j];
+    __syncthreads();
+    if (fallback) {
+      // Top-1: video -> scores.argmax(dim=-1) over the full row, the first NaN if there is
+      // one, else the first maximum (-0 == +0); joint -> sorted_indices[..., 0], the
+      // candidate of the largest key, from the exact std::sort order when the top two keys
+      // tie.  Without such a tie both are the largest (order_key, ~index) pair of the row.
+      const uint8_t flags = a.ws_flags[rid];
+      const float* src = a.scores + (int64_t)rid * nk;
+      const bool video = a.mode == 1;
+      int t;
+      if (flags & 2) {
+        uint64_t* e = pe + 1;
+        for (int j = lane; j < nk; j += 64) {
+          const bool req = (qb < a.req_q) || (j < a.req_k);
+          e[j] = pmake(req ? neg_inf() : src[j], j);
+        }
+        __syncthreads();
+        wave_sort_positions(e, nk, 0, 1, stk, lrp, lrp + NMAX, lane);
+        t = pidx(pe[1]);
+      } else {
+        uint64_t best = 0ull;
+        for (int j = lane; j < nk; j += 64) {
+          const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
+          const uint64_t key = ((uint64_t)order_key(req ? neg_inf() : src[j]) << 32) | (uint64_t)(~(uint32_t)j);
+          best = key > best ? key : best;
+        }
+        best = wave_max_u64(best);
+        t = (int)(~(uint32_t)(best & 0xffffffffull));
+      }
+      if (lane == 0) {
+        m[t] = flags & 1;
+        mrow[t] = flags & 1;
       }
       __syncthreads();
-      wave_sort_positions(e, nk, 0, 1, stk, lrp, lrp + NMAX, lane);
-      t = pidx(pe[1]);
-    } else {
-      uint64_t best = 0ull;
-      for (int j = lane; j < nk; j += 64) {
-        const bool req = !video && ((qb < a.req_q) || (j < a.req_k));
-        const uint64_t key = ((uint64_t)order_key(req ? neg_inf() : src[j]) << 32) | (uint64_t)(~(uint32_t)j);
-        best = key > best ? key : best;
+    }
+    if (a.idx != nullptr || a.counts != nullptr) {
+      int base = 0;
+      for (int c0 = 0; c0 < nk; c0 += 64) {
+        const int j = c0 + lane;
+        const bool on = j < nk && m[j];
+        const uint64_t bal = __ballot(on);
+        if (on && a.idx != nullptr)
+          a.idx[(int64_t)rid * nk + base + __popcll(bal & ((1ull << lane) - 1ull))] = j;
+        base += __popcll(bal);
       }
-      best = wave_max_u64(best);
-      t = (int)(~(uint32_t)(best & 0xffffffffull));
+      if (lane == 0 && a.counts != nullptr) a.counts[rid] = base;
     }
-    if (lane == 0) {
-      m[t] = flags & 1;
-      mrow[t] = flags & 1;
-    }
-    __syncthreads();
-  }
-  if (a.idx != nullptr || a.counts != nullptr) {
-    int base = 0;
-    for (int c0 = 0; c0 < nk; c0 += 64) {
-      const int j = c0 + lane;
-      const bool on = j < nk && m[j];
-      const uint64_t bal = __ballot(on);
-      if (on && a.idx != nullptr)
-        a.idx[(int64_t)rid * nk + base + __popcll(bal & ((1ull << lane) - 1ull))] = j;
-      base += __popcll(bal);
-    }
-    if (lane == 0 && a.counts != nullptr) a.counts[rid] = base;
+    __syncthreads();  // m is refilled for the next row
   }
 }
 
@@ -947,7 +954,7 @@ static hipError_t launch_mask_c(const MaskArgs& a, int rows, hipStream_t stream)
   coverage_mask_kernel<C><<<rows, 64, 0, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  coverage_fixup_kernel<C><<<rows, 64, 0, stream>>>(a);
+  coverage_fixup_kernel<C><<<(int)(((int64_t)rows + kFixupRows - 1) / kFixupRows), 64, 0, stream>>>(a);
   return hipGetLastError();
 }
 
