@@ -557,6 +557,11 @@ __device__ __forceinline__ void lane_stage(uint32_t (&kk)[C][4], int size, int l
 template <int C>
 __device__ __forceinline__ void bitonic_sort_regs(uint32_t (&kk)[C][4], int lane) {
   constexpr int P = 256 * C;
+  // Short networks are unrolled whole (every distance and direction a constant, no loop
+  // or switch control on the scalar unit); long ones keep the loops to bound code size.
+  constexpr int kUnrollSizes = C <= 2 ? 16 : 1;
+  constexpr int kUnrollStrides = C <= 2 ? 8 : 1;
+#pragma unroll kUnrollSizes
   for (int size = 2; size <= P; size <<= 1) {
     // Distances of 256 and up, longest first, each chunk distance a compile-time constant
     // (as separate steps rather than one indexed step, so every key stays in a register).
@@ -572,6 +577,7 @@ __device__ __forceinline__ void bitonic_sort_regs(uint32_t (&kk)[C][4], int lane
     if constexpr (C >= 2) {
       if (size >= 512) chunk_stage<C, 1>(kk, size);
     }
+#pragma unroll kUnrollStrides
     for (int stride = min(size >> 1, 128); stride >= 4; stride >>= 1) {
       switch (stride) {
         case 128: xlane_stage<C, 32>(kk, size, lane); break;
