@@ -262,3 +262,22 @@ def test_non_finite_scores(mode):
     vt = tb if mode == "video_residual" else None
     got = ops.coverage_mask(s.cuda(), 0.85, True, tb, tb, vt)
     assert torch.equal(got.cpu(), ref)
+
+
+def test_wan_pooled_map_bit_exact():
+    # A full Wan-size pooled map (B2 H12 N32760, frame-0 keys as sinks) averaged over the
+    # batch as the calibrator does: near-uniform rows, deep cuts and, for this seed, rows
+    # whose cut splits equal values (the tie-exact path on realistic data).
+    torch.manual_seed(0)
+    q = torch.randn(2, 12, 32760, 128, device="cuda", dtype=torch.bfloat16)
+    k = torch.randn(2, 12, 32760, 128, device="cuda", dtype=torch.bfloat16)
+    k[:, :, :1560] *= 3.0
+    cfg = sa.SinkSparseConfig(pooling_mode="exact")
+    s = sa._compute_block_scores(q, k, k, cfg).float().mean(dim=0).contiguous()
+    del q, k
+    ref = torch_ref.coverage_mask(s.cpu())
+    got, counts, idx = ops.coverage_mask(s, 0.85, True, want_lists=True)
+    assert torch.equal(got.cpu(), ref)
+    _check_lists(got, counts, idx)
+    # the drop-in entry point with the reference's CPU tensors
+    assert torch.equal(sa._build_direct_mean_coverage_mask(s.cpu(), cfg), ref)
