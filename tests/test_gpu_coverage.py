@@ -281,3 +281,21 @@ def test_wan_pooled_map_bit_exact():
     _check_lists(got, counts, idx)
     # the drop-in entry point with the reference's CPU tensors
     assert torch.equal(sa._build_direct_mean_coverage_mask(s.cpu(), cfg), ref)
+
+
+def test_zimage_pooled_map_bit_exact():
+    # A Z-Image-shaped pooled map (H30, 16384 image + 512 text tokens, text keys x4 as
+    # sinks) through the drop-in with the required text rows and columns.
+    torch.manual_seed(1)
+    n_img, n_txt = 16384, 512
+    q = torch.randn(1, 30, n_img + n_txt, 128, device="cuda", dtype=torch.bfloat16)
+    k = torch.randn(1, 30, n_img + n_txt, 128, device="cuda", dtype=torch.bfloat16)
+    k[:, :, :n_txt] *= 4.0
+    cfg = sa.SinkSparseConfig(pooling_mode="exact", text_length=n_txt, force_text_global_attention=True)
+    s = sa._compute_block_scores(q, k, k, cfg).float().mean(dim=0).contiguous()
+    del q, k
+    assert s.shape == (30, 132, 132)
+    ref = torch_ref.coverage_mask(s.cpu(), text_length=n_txt, force_text=True)
+    assert torch.equal(sa._build_direct_mean_coverage_mask(s.cpu(), cfg), ref)
+    got = ops.coverage_mask(s, 0.85, True, 4, 4)
+    assert torch.equal(got.cpu(), ref)
