@@ -4,6 +4,10 @@ Mirrors the interface of the reference's AttentionTimingCollector
 (sinkattention/timing.py:12-100) that SinkRuntimeState.time_section hands out: the
 section(name) context manager, summarize(), reset() and is_enabled.  Enabled by
 SINK_ATTN_ENABLE_TIMING (or WAN_ATTN_ENABLE_TIMING) set to 1/true/yes/on.
+
+Also the two summary helpers the Wan inference CLI imports
+(wanx/runtime/inference.py:23): extract_attention_time_ms and
+aggregate_timing_summaries (sinkattention/timing.py:103-169).
 """
 from __future__ import annotations
 
@@ -11,7 +15,7 @@ import os
 import time
 from collections import defaultdict
 from contextlib import contextmanager
-from typing import Dict, List, Optional, Tuple
+from typing import Dict, Iterable, List, Optional, Tuple
 
 import torch
 
@@ -80,3 +84,53 @@ class AttentionTimingCollector:
                                "count": cnt[n]} for n in names},
             "total_ms": float(sum(tot.values())),
         }
+
+
+def extract_attention_time_ms(
+    summary: Optional[dict],
+    *,
+    preferred_sections: Iterable[str] = ("inner_total",),
+) -> Optional[float]:
+    """Attention time of one summarize() result (sinkattention/timing.py:103-123).
+
+    None for a missing or disabled summary; else the total of the first preferred section
+    that has one, else the summary's own total (None when that is absent).
+    """
+    if not summary or not summary.get("enabled", False):
+        return None
+    sections = summary.get("by_section") or {}
+    for name in preferred_sections:
+        entry = sections.get(name)
+        if entry is not None and entry.get("total_ms") is not None:
+            return float(entry["total_ms"])
+    total = summary.get("total_ms")
+    return None if total is None else float(total)
+
+
+def aggregate_timing_summaries(summaries: Iterable[Optional[dict]]) -> Optional[dict]:
+    """Mean / max / sum over several summarize() results (sinkattention/timing.py:126-169).
+
+    Disabled or empty summaries are skipped; None when none is left.  Per-section statistics
+    are keyed by str(section name) in sorted order; the totals skip entries without total_ms.
+    """
+    kept = [s for s in summaries if s and s.get("enabled", False)]
+    if not kept:
+        return None
+    per_section: Dict[str, List[float]] = defaultdict(list)
+    totals: List[float] = []
+    for s in kept:
+        if s.get("total_ms") is not None:
+            totals.append(float(s["total_ms"]))
+        for name, entry in (s.get("by_section") or {}).items():
+            if entry.get("total_ms") is not None:
+                per_section[str(name)].append(float(entry["total_ms"]))
+    names = sorted(n for n in per_section if per_section[n])
+    return {
+        "count": len(kept),
+        "labels": sorted({str(s.get("label", "")) for s in kept if s.get("label")}),
+        "mean_total_ms": sum(totals) / len(totals) if totals else None,
+        "max_total_ms": max(totals) if totals else None,
+        "mean_by_section_ms": {n: sum(per_section[n]) / len(per_section[n]) for n in names},
+        "max_by_section_ms": {n: max(per_section[n]) for n in names},
+        "total_by_section_ms": {n: float(sum(per_section[n])) for n in names},
+    }
