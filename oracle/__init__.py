@@ -17,7 +17,11 @@ c_ref       ctypes loader of oracle/_build/liboracle.so: the plain-C coverage-ma
 How each function is pinned (tests/test_oracle_*.py):
   exact block mass     fp64 brute force on small shapes; closed forms (rows sum to 1,
                        Q = 0 gives |kb|/N, a dominant sink key gives block 0 -> 1)
-  max-pool             fp64 evaluation of the formula, row normalisation invariant
+  max-pool             the reference kernel's own outputs (tests/golden/max_pool.npz, its
+                       Triton source run by Triton's CPU interpreter in float16): bit for
+                       bit on inputs whose q.k are exact in fp32, and each of the four
+                       rounding points, left out, breaks them; fp64 evaluation of the
+                       formula; row normalisation invariant
   mean-pooled scores   closed form (softmax of pooled dot products, padding rule)
   coverage mask        C model vs torch on this machine (sum order, cumsum, sort
                        permutation incl. ties), emulated vs real std::sort, brute-force
@@ -29,7 +33,7 @@ How each function is pinned (tests/test_oracle_*.py):
                        gap 1 and equal LSEs
   K/V mean pooling     ramp and constant closed forms, replicate-padded last group,
                        prefix rows untouched, identities at gap 1 / prefix >= N
-Parity unpinned: the bf16 bit pattern of the reference Triton max-pool kernel
-(``attn_with_pooling``) beyond "within bf16 rounding", and its ragged-N behaviour
-(undefined in the reference).
+Not pinned by a reference output: the max-pool map in bf16 (Triton's interpreter mishandles
+bf16, so the fixtures are float16; bf16 differs only in the rounding format, checked to be
+round-to-nearest-even), and its ragged-N behaviour (undefined in the reference).
 """

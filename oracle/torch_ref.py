@@ -78,12 +78,16 @@ def exact_block_mass_fp64(q: torch.Tensor, k: torch.Tensor, block_size: int = 12
 # row sum rounded to q.dtype, the division rounded to q.dtype.
 # ---------------------------------------------------------------------------------------
 def max_pool_map(q: torch.Tensor, k: torch.Tensor, sm_scale: float, block_size: int = 128,
-                 causal: bool = False, exact: bool = False, query_blocks=None) -> torch.Tensor:
+                 causal: bool = False, exact: bool = False, query_blocks=None,
+                 skip_rounding=()) -> torch.Tensor:
     """exact=True evaluates the formula in float64 without any rounding.
 
     query_blocks (optional): the query-block indices to evaluate, in order; the result
     then holds those rows of the map only.  Each query block is computed on its own
     (rows of the map are independent), so long sequences fit in memory.
+
+    skip_rounding (tests only): names among "R", "Po", "sum", "div" whose rounding to
+    q.dtype is left out, so a test can show that the golden fixtures detect each one.
     """
     dt = q.dtype
     work = torch.float64 if exact else torch.float32
@@ -114,15 +118,18 @@ def max_pool_map(q: torch.Tensor, k: torch.Tensor, sm_scale: float, block_size: 
         if causal:
             bmax[..., qbi + 1:] = float("-inf")
         m = bmax.amax(-1, keepdim=True)
-        r = bmax if exact else bmax.to(dt).to(work)
+        r = bmax if exact or "R" in skip_rounding else bmax.to(dt).to(work)
         po[:, :, i] = torch.exp2(r - m).amax(dim=2)
         if causal:
             po[:, :, i, qbi + 1:] = 0.0
     if exact:
         return po / po.sum(-1, keepdim=True)
-    po = po.to(dt)
-    tot = po.float().sum(-1, keepdim=True).to(dt)
-    return (po.float() / tot.float()).to(dt)
+    po = po.float() if "Po" in skip_rounding else po.to(dt).float()
+    tot = po.sum(-1, keepdim=True)
+    if "sum" not in skip_rounding:
+        tot = tot.to(dt).float()
+    out = po / tot
+    return out if "div" in skip_rounding else out.to(dt)
 
 
 # ---------------------------------------------------------------------------------------

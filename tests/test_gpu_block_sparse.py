@@ -124,6 +124,35 @@ def test_config1_shape_fp32_with_sinks():
     _check(out, lse[..., 0], q, k, v, mask, rows=rows)
 
 
+def test_config1_chain_mass_mask_attention():
+    """BASELINE config 1 as one chain: exact block mass -> coverage-0.85 mask -> sparse
+    attention on that mask (sparse_attention.py:145-227, 268-376, 710-776).
+
+    fp32 [1,12,4096,128], keys 0..3 x8.  Mass within 1e-5 relative of the oracle; the mask
+    bit-exact with the oracle's builder on the same pooled map; attention on that mask within
+    2e-2 / 1e-3 of the dense masked softmax (1024 rows per head)."""
+    q, k, v = _inputs(1, 12, 4096, 4096, 128, torch.float32, seed=0, sink_keys=4)
+    cfg = sa.SinkSparseConfig(pooling_mode="exact", offline_direct_coverage=0.85)
+    mass = sa._compute_block_scores(q, k, v, cfg)
+    torch.cuda.synchronize()
+    assert mass.shape == (1, 12, 32, 32) and mass.dtype == torch.float32
+    ref = torch_ref.exact_block_mass(q, k).double()
+    rel = ((mass.cpu().double() - ref).abs() / ref.abs().clamp_min(1e-30))
+    assert bool(((mass.cpu().double() - ref).abs() <= 1e-5 * ref.abs() + 1e-8).all()), rel.max().item()
+    mean_scores = mass.mean(dim=0)                                # batch mean, [12, 32, 32]
+    mask = sa._build_direct_mean_coverage_mask(mean_scores, cfg)
+    assert mask.dtype == torch.bool and mask.is_cuda
+    want = torch_ref.coverage_mask(mean_scores.cpu(), coverage=0.85, keep_diagonal=True)
+    assert torch.equal(mask.cpu(), want)
+    density = mask.float().mean().item()
+    assert 0.0 < density < 1.0, density                           # the sinks make it sparse
+    block_mask = mask.unsqueeze(0).expand(1, -1, -1, -1)
+    out, lse = sa._block_sparse_attn(q, k, v, block_mask, return_lse=True)
+    torch.cuda.synchronize()
+    rows = torch.randperm(4096, generator=torch.Generator().manual_seed(1))[:1024].sort().values
+    _check(out, lse[..., 0], q, k, v, block_mask, rows=rows)
+
+
 def test_full_mask_equals_dense_sdpa():
     q, k, v = _inputs(2, 4, 640, 640, 128, torch.bfloat16, seed=5)
     mask = torch.ones(2, 4, 5, 5, dtype=torch.bool, device="cuda")
