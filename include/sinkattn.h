@@ -258,6 +258,33 @@ int sinkattn_coverage_mask(const float* scores, int64_t H, int64_t nq, int64_t n
                            uint8_t* mask, int32_t* counts, int32_t* idx,
                            void* workspace, void* stream);
 
+/* ------------------------------------------------------------------------------------
+ * Block-sparse forward from a bool mask, allocating nothing.
+ *
+ * No counterpart in the reference.  It is for callers that cannot allocate device memory:
+ * code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * Same as sinkattn_block_sparse_plan followed by sinkattn_block_sparse_fwd (same checks,
+ * kernels and results), but the plan (counts, index lists, launch order) is kept in a
+ * static device array of SINKATTN_NOALLOC_SCRATCH_BYTES that the library owns, one per GPU,
+ * held until the process ends.  The caller passes the mask (uint8/bool
+ * [B,H,ceil(Nq/128),ceil(Nk/128)] with element strides, as for the plan) and the inputs and
+ * outputs (as for the forward).  No device memory is allocated or freed.
+ * Limit: 4 bytes per row for the counts, 4 per launch slot, and 4 * nkb per row for the
+ * lists must fit the 32 MiB array: about 8 million mask entries B*H*nqb*nkb (Wan config 2
+ * needs 1.6 million).  Larger calls return an invalid-argument status.
+ * The array keeps the last call's plan and is shared by all calls on one GPU: calls on one
+ * stream are ordered, but calls that overlap on one GPU (several streams or threads at
+ * once) race and must not be issued.
+ * ---------------------------------------------------------------------------------- */
+#define SINKATTN_NOALLOC_SCRATCH_BYTES (32u << 20)
+int sinkattn_block_sparse_attn_noalloc(const uint8_t* mask, const int64_t mask_strides[4],
+                                       const void* q, const void* k, const void* v, int dtype,
+                                       int64_t B, int64_t H, int64_t Nq, int64_t Nk, int64_t D,
+                                       const int64_t q_strides[4], const int64_t k_strides[4],
+                                       const int64_t v_strides[4], void* out,
+                                       const int64_t out_strides[4], float* lse,
+                                       float softmax_scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

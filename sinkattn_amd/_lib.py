@@ -83,6 +83,11 @@ SIGNATURES = {
         [_c_p, _c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64_4, _c_i64_4,
          _c_i64, ctypes.c_float, _c_p, _c_p, _c_p],
     ),
+    "sinkattn_block_sparse_attn_noalloc": (
+        ctypes.c_int,
+        [_c_p, _c_i64_4, _c_p, _c_p, _c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64_4, _c_i64_4, _c_i64_4, _c_p, _c_i64_4, _c_p, ctypes.c_float, _c_p],
+    ),
     "sinkattn_coverage_mask_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64]),
     "sinkattn_coverage_mask": (
         ctypes.c_int,

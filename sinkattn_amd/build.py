@@ -27,6 +27,7 @@ SOURCES = [
     "coverage_mask.hip",
     "compensation.hip",
     "qk_prep.hip",
+    "noalloc.hip",
     "capi.cpp",
 ]
 

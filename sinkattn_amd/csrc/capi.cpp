@@ -51,6 +51,22 @@ const int64_t kMaxInt = 0x7fffffffLL;
 
 }  // namespace
 
+namespace sa {
+
+int api_fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return -1;
+}
+
+int api_hip_status(hipError_t e, const char* what) { return hip_status(e, what); }
+
+}  // namespace sa
+
 extern "C" {
 
 const char* sinkattn_last_error(void) { return g_last_error.c_str(); }

@@ -125,4 +125,10 @@ hipError_t launch_mean_pool_tokens(const TokenPoolArgs& a, int dtype, hipStream_
 hipError_t launch_lse_mix(const MixArgs& a, int dtype, hipStream_t stream);
 hipError_t launch_qk_prep(const QkPrepArgs& a, int dtype, hipStream_t stream);
 
+// The C ABI's status channel (capi.cpp): api_fail stores a printf-style message for
+// sinkattn_last_error() and returns -1; api_hip_status returns 0 for hipSuccess, else stores
+// "<what>: <HIP message>" and returns the error code.
+int api_fail(const char* fmt, ...);
+int api_hip_status(hipError_t e, const char* what);
+
 }  // namespace sa

@@ -1,0 +1,108 @@
+"""sinkattn_block_sparse_attn_noalloc (the forward from a bool mask with the plan in the
+library's static device array) against sinkattn_block_sparse_plan + sinkattn_block_sparse_fwd
+with caller buffers, both through the C ABI.
+
+The two run the same kernels on the same plan, so the outputs must be bit-identical.  Two calls
+in a row, the second on a smaller input (the static array still holds the first call's larger
+plan), then the first shape again; plus the size limit, which is checked on the host before
+any launch."""
+import ctypes
+import math
+
+import pytest
+import torch
+
+from sinkattn_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, H, N, dtype, seed, density):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(B, H, N, 128, generator=g).to("cuda", dtype) for _ in range(3))
+    nb = math.ceil(N / 128)
+    mask = torch.rand(B, H, nb, nb, generator=g) < density
+    d = torch.arange(nb)
+    mask[:, :, d, d] = True
+    mask[0, 0, nb // 2] = False                     # one empty row
+    return q, k, v, mask.cuda()
+
+
+def _outputs(q):
+    B, H, N, D = q.shape
+    out = torch.full((B, N, H, D), float("nan"), dtype=q.dtype, device=q.device).permute(0, 2, 1, 3)
+    lse = torch.full((B, H, N), float("nan"), dtype=torch.float32, device=q.device)
+    return out, lse
+
+
+def _noalloc(q, k, v, mask):
+    lib = _lib.lib()
+    B, H, Nq, D = q.shape
+    out, lse = _outputs(q)
+    m = mask.to(torch.uint8)
+    rc = lib.sinkattn_block_sparse_attn_noalloc(
+        m.data_ptr(), _lib.strides4(m), q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.dtype_code(q.dtype),
+        B, H, Nq, k.shape[2], D, _lib.strides4(q), _lib.strides4(k), _lib.strides4(v),
+        out.data_ptr(), _lib.strides4(out), lse.data_ptr(), 1.0 / math.sqrt(D), _lib.stream_ptr(q.device))
+    _lib.check(rc, "sinkattn_block_sparse_attn_noalloc")
+    return out, lse
+
+
+def _with_plan(q, k, v, mask):
+    lib = _lib.lib()
+    B, H, Nq, D = q.shape
+    Nk = k.shape[2]
+    nqb, nkb = mask.shape[2], mask.shape[3]
+    m = mask.to(torch.uint8)
+    counts = torch.empty(B * H * nqb, dtype=torch.int32, device=q.device)
+    idx = torch.empty(B * H * nqb * nkb, dtype=torch.int32, device=q.device)
+    order = torch.empty(lib.sinkattn_block_sparse_order_slots(B, H, nqb), dtype=torch.int32, device=q.device)
+    stream = _lib.stream_ptr(q.device)
+    _lib.check(lib.sinkattn_block_sparse_plan(m.data_ptr(), _lib.strides4(m), B, H, nqb, nkb, counts.data_ptr(),
+                                              idx.data_ptr(), order.data_ptr(), stream), "plan")
+    out, lse = _outputs(q)
+    _lib.check(lib.sinkattn_block_sparse_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.dtype_code(q.dtype), B, H, Nq, Nk, D,
+        _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), out.data_ptr(), _lib.strides4(out),
+        lse.data_ptr(), counts.data_ptr(), idx.data_ptr(), order.data_ptr(), nqb, nkb, 1.0 / math.sqrt(D),
+        stream), "fwd")
+    return out, lse
+
+
+def _same(a, b):
+    return torch.equal(a.view(torch.int16) if a.dtype != torch.float32 else a.view(torch.int32),
+                       b.view(torch.int16) if b.dtype != torch.float32 else b.view(torch.int32))
+
+
+def test_noalloc_matches_plan_and_forward_twice_then_smaller():
+    big = _inputs(2, 6, 3000, torch.bfloat16, seed=1, density=0.3)
+    small = _inputs(1, 2, 700, torch.bfloat16, seed=2, density=0.5)
+    for q, k, v, mask in (big, small, big):
+        print(f"noalloc vs plan+fwd: q {tuple(q.shape)} mask {tuple(mask.shape)}", flush=True)
+        got_o, got_l = _noalloc(q, k, v, mask)
+        want_o, want_l = _with_plan(q, k, v, mask)
+        torch.cuda.synchronize()
+        assert not torch.isnan(got_o).any() and not torch.isnan(got_l).any()
+        assert _same(got_o, want_o)
+        assert _same(got_l, want_l)
+        assert torch.isinf(got_l[0, 0, (mask.shape[2] // 2) * 128]).item()   # the empty row
+
+
+def test_noalloc_f16_bshd_views():
+    q, k, v, mask = _inputs(1, 4, 1000, torch.float16, seed=3, density=0.4)
+    q, k, v = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
+    got = _noalloc(q, k, v, mask)
+    want = _with_plan(q, k, v, mask)
+    torch.cuda.synchronize()
+    assert _same(got[0], want[0]) and _same(got[1], want[1])
+
+
+def test_noalloc_rejects_plans_beyond_the_static_buffer():
+    lib = _lib.load_library()
+    z = (ctypes.c_int64 * 4)(0, 0, 0, 1)
+    # 2 x 40 x 591 x 591 blocks (Wan-14B 720p) needs ~112 MB of plan: refused before any launch
+    rc = lib.sinkattn_block_sparse_attn_noalloc(None, z, None, None, None, 0, 2, 40, 75600, 75600, 128,
+                                                z, z, z, None, z, None, 0.088, None)
+    assert rc < 0
+    msg = lib.sinkattn_last_error().decode()
+    assert "static plan buffer" in msg and "sinkattn_block_sparse_plan" in msg
