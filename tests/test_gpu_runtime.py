@@ -4,9 +4,10 @@ The oracle side follows the reference's precision where it rounds on purpose: th
 pooled K/V of the compensation branch are bf16 tensors there and both LSEs are cast to
 q.dtype (sparse_attention.py:776) before the mix, so the oracle rounds the same values
 to bf16 at the same points and computes everything else in fp32.  Tolerances: the
-block-sparse output 2e-2 max-abs / 1e-3 mean-abs (the attention bar); the mixed output
-3e-2 max-abs / 2e-3 mean-abs, because a bf16 LSE that rounds to the neighbouring value
-on one side shifts the mixing weight by up to ~1.5% on that row."""
+attention output 2e-2 max-abs / 1e-3 mean-abs (the attention bar), also for the installed
+processors' outputs, with and without the output projection; the unfused reference sequence
+(and the fused kernel compared with it) within `_check_rounded_mix`'s bound, because a bf16 LSE
+that rounds to the neighbouring value on one side shifts the mixing weight on that row."""
 import math
 
 import pytest
@@ -90,6 +91,10 @@ def test_wan_inner_attention_vs_oracle(mode, text, band, fuse, monkeypatch):
     elif fuse:  # one kernel: the exact fp32 mix of the two branches
         _check(out, _expected_wan(qc, kc, vc, mask, cfg, round_lse=False), 2e-2, 1e-3,
                f"wan fused text={text} band={band}")
+        # and against the reference's own sequence (both LSEs rounded to bf16 before the mix):
+        # the fused kernel departs from it only by those roundings
+        want, so, sl, do, dl, gap = _expected_wan(qc, kc, vc, mask, cfg, parts=True)
+        _check_rounded_mix(out, want, so, sl, do, dl, gap, f"wan fused vs reference-rounded text={text}")
     else:
         want, so, sl, do, dl, gap = _expected_wan(qc, kc, vc, mask, cfg, parts=True)
         _check_rounded_mix(out, want, so, sl, do, dl, gap, f"wan unfused text={text} band={band}")
@@ -146,10 +151,21 @@ def test_wan_processor_installed_model(tmp_path):
         inner = blk.attn1.inner_attention
         mask = inner._get_runtime_mask(inner.sink_mask, "__base__", 1, H, N, N, q.device).cpu()
         o = _expected_wan(q.float().cpu(), k.float().cpu(), v.float().cpu(), mask, inner.config, round_lse=False)
-        o = o.transpose(1, 2).flatten(2, 3).to(DEV, torch.bfloat16)
-        want = blk.attn1.to_out[0](o).float().cpu()
-        _check(out, want, 6e-2, 4e-3, f"wan processor layer {i}")
-    assert model._sink_runtime_state.current_step == 0 and len(model._sink_runtime_state.sparsity_events) == 2
+        o_rows = o.transpose(1, 2).flatten(2, 3)
+        want = blk.attn1.to_out[0](o_rows.to(DEV, torch.bfloat16)).float().cpu()
+        # after the output projection
+        _check(out, want, 2e-2, 1e-3, f"wan processor layer {i}")
+        # the attention output itself, with the projection taken out: the attention bar
+        proj = blk.attn1.to_out[0]
+        blk.attn1.to_out[0] = nn.Identity()
+        try:
+            att = blk.attn1(x, rotary_emb=freqs)
+            torch.cuda.synchronize()
+        finally:
+            blk.attn1.to_out[0] = proj
+        _check(att, o_rows, 2e-2, 1e-3, f"wan processor layer {i} attention output")
+    # layer 0 ran twice (with and without the projection): two steps, four events
+    assert model._sink_runtime_state.current_step == 1 and len(model._sink_runtime_state.sparsity_events) == 4
 
 
 class _ZAttn(nn.Module):
@@ -203,6 +219,12 @@ def test_zimage_static_processor_vs_oracle(mode):
         amask[b, :n] = True
     out = proc(attn, x, attention_mask=amask)
     torch.cuda.synchronize()
+    # the attention output itself: the same call with the output projection taken out
+    proj = attn.to_out[0]
+    attn.to_out[0] = nn.Identity()
+    att = proc(attn, x, attention_mask=amask)
+    torch.cuda.synchronize()
+    attn.to_out[0] = proj
     q, k, v = zr.prepare_zimage_attention_tensors(attn, x)
     for b, n in enumerate(lens):
         tb = -(-(n - image_tokens) // 128)
@@ -211,12 +233,15 @@ def test_zimage_static_processor_vs_oracle(mode):
             image_blocks=ib, current_text_blocks=tb).unsqueeze(0)
         qs, ks, vs = (t[b:b + 1, :n].permute(0, 2, 1, 3).float().cpu() for t in (q, k, v))
         o = _zimage_expected(qs, ks, vs, m, cfg, image_tokens, n)
-        want_rows = attn.to_out[0](o.transpose(1, 2).flatten(2, 3).to(DEV, torch.bfloat16)).float().cpu()[0]
-        _check(out[b, :n], want_rows, 6e-2, 4e-3, f"zimage {mode} sample {b} len {n}")
+        o_rows = o.transpose(1, 2).flatten(2, 3)[0]
+        want_rows = attn.to_out[0](o_rows.to(DEV, torch.bfloat16)).float().cpu()
+        # after the output projection
+        _check(out[b, :n], want_rows, 2e-2, 1e-3, f"zimage {mode} sample {b} len {n}")
+        _check(att[b, :n], o_rows, 2e-2, 1e-3, f"zimage {mode} sample {b} attention output")
         pad = attn.to_out[0](torch.zeros(1, H * D, device=DEV, dtype=torch.bfloat16)).float().cpu()
         if n < Nmax:
             assert torch.allclose(out[b, n:].float().cpu(), pad.expand(Nmax - n, -1), atol=1e-2)
-    assert len(state.sparsity_events) == 3
+    assert len(state.sparsity_events) == 6
     # masks are cached per text-block count: 3 distinct lengths -> 3 entries
     assert len(proc._runtime_mask_cache) == 3
 
