@@ -170,256 +170,316 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_kernel(FwdArgs a) {
 // ------------------------------------------------------------------------------------
 constexpr float kLazyRescaleLog2 = 8.0f;
 
+// Per-lane LDS addresses of the d128 tile loop (bytes): the DMA destination offsets of this
+// wave's copies, the K rows of the S^T A operand, and the V^T transpose reads.
+struct D128Lanes {
+  uint32_t k_off, v_off;  // global byte offset of this lane's first 16-byte DMA chunk
+  uint32_t ka[8];         // K: MFMA row t*32 + k_row_perm(l32), chunk 2ds + hl (+ t * 8192)
+  uint32_t va[4][2];      // V^T transpose reads of d-tile dt
+};
+
+__device__ __forceinline__ D128Lanes d128_lanes(int wave, int lane, uint32_t kstride, uint32_t vstride) {
+  D128Lanes L;
+  const int hl = lane >> 5, l32 = lane & 31;
+  // DMA: instruction j of wave w fills tile rows 16j + 4w + lane/16 (LDS bytes
+  // [(256j + 64w) * 16, +1024)); the swizzle of those rows does not depend on j.
+  const int drow = 4 * wave + (lane >> 4);
+  L.k_off = (uint32_t)drow * kstride + (uint32_t)(((lane & 15) ^ (drow & 15)) * 16);
+  L.v_off = (uint32_t)drow * vstride + (uint32_t)(((lane & 15) ^ (4 * (drow & 3))) * 16);
+  const int prow = k_row_perm(l32);
+#pragma unroll
+  for (int ds = 0; ds < 8; ++ds) L.ka[ds] = (uint32_t)(prow * 256 + (((2 * ds + hl) ^ (prow & 15)) * 16));
+  // V^T via transpose reads: 16-lane group g, lane s in group -> source row
+  // 8*(g/2) + 4r + s/4 (+16u + 32t), columns dt*32 + 16*(g%2) + 4*(s%4) .. +3.
+  const int g = lane >> 4, sl = lane & 15;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int row = 8 * (g >> 1) + 4 * r + (sl >> 2);
+      const int chunk = dt * 4 + 2 * (g & 1) + ((sl & 3) >> 1);
+      const int phys = chunk ^ (4 * (row & 3));
+      L.va[dt][r] = (uint32_t)(row * 256 + phys * 16 + (sl & 1) * 8);
+    }
+  return L;
+}
+
+// 128 rows of K (or V) from `base` (row stride `stride` bytes, `rows_valid` rows readable:
+// rows past it read as zero through the buffer bounds) into the LDS tile at `dst`.
+__device__ __forceinline__ void d128_copy_tile(SA_LDS char* dst, const char* base, uint32_t stride,
+                                               int rows_valid, uint32_t lane_off, int wave) {
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)rows_valid * stride);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    dma16(rs, (SA_LDS void*)(dst + (256 * j + 64 * wave) * 16), lane_off + (uint32_t)j * 16u * stride);
+}
+
+// One 128-key tile of the d128 loop for this wave's 32 query rows:
+//   S^T = K Q^T from the K tile, barrier B1 (V has landed, every wave is done with K),
+//   after_b1() (the K buffer is free: the next K copy goes there), the online softmax,
+//   O^T += V^T P^T from the V tile, barrier B2 (the next K has landed, every wave is done
+//   with V), after_b2() (the V buffer is free).
+// Keys at or past klim are masked; bias is added to the log2-domain logits (compensation
+// tiles); c = softmax scale * log2(e).
+template <int CT, typename FB1, typename FB2>
+__device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, const D128Lanes& L,
+                                          const u32x4 (&qf)[8], int key0, int klim, float bias,
+                                          float c, int hl, f32x16 (&o)[4], float& m_run,
+                                          float& l_run, FB1&& after_b1, FB2&& after_b2) {
+  constexpr int DS = 8, DT = 4;
+  f32x16 s[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) s[t] = f32x16{};
+  {
+    // Reads for k-step ds+1 are issued between the MFMAs of k-step ds, one read after
+    // each MFMA; the scheduling groups pin that order so no MFMA waits on the read
+    // issued just before it.
+    u32x4 kr[2][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) kr[0][t] = *(SA_LDS const u32x4*)(lk + L.ka[0] + t * 8192);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        s[t] = mfma32x32x16<CT>(kr[ds & 1][t], qf[ds], s[t]);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (ds + 1 < DS) {
+          kr[(ds + 1) & 1][t] = *(SA_LDS const u32x4*)(lk + L.ka[ds + 1] + t * 8192);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      }
+    }
+  }
+  drain_then_barrier();  // B1
+  after_b1();
+
+  if (key0 + 128 > klim) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (key0 + t * 32 + tile_key(hl, j) >= klim) s[t][j] = neg_inf();
+  }
+  float mx = neg_inf();
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
+  mx = max_xor32(mx);
+  // Lazy rescale: the reference point m_run moves only when this tile's maximum exceeds
+  // it by more than kLazyRescaleLog2, so P = exp2(c*s + bias - m_run) stays at most 2^8
+  // (well inside the range of bf16/f16 P and fp32 O, l) and the 64 multiplies of O run
+  // on few tiles.  O / l and m_run + log2(l) do not depend on the reference point.
+  const float m_tile = __builtin_fmaf(mx, c, bias);
+  if (m_tile > m_run + kLazyRescaleLog2) {
+    const float alpha = fast_exp2(m_run - m_tile);
+    l_run *= alpha;
+#pragma unroll
+    for (int i = 0; i < DT; ++i) o[i] *= alpha;
+    m_run = m_tile;
+  }
+  // P in the MFMA's 16-bit type; the row sum adds those rounded values (one dot2 per
+  // pair, four independent partial sums), so O and l are normalised by the same weights.
+  u32x4 p[4][2];
+  float lsum[4] = {0.f, 0.f, 0.f, 0.f};
+  auto make_p = [&](int t, int u) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float v0 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e], c, bias - m_run));
+      const float v1 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e + 1], c, bias - m_run));
+      p[t][u][e] = pack2<CT>(v0, v1);
+      lsum[t] = sum2_acc<CT>(p[t][u][e], lsum[t]);
+    }
+  };
+  // V^T operand for d-tile dt of step (t, u): two transpose reads.
+  auto vread = [&](int dt, int t, int u) -> u32x4 {
+    const uint32_t off = t * 8192 + u * 4096;
+    const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + L.va[dt][0] + off));
+    const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + L.va[dt][1] + off));
+    const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
+    return u32x4{y0[0], y0[1], y1[0], y1[1]};
+  };
+  make_p(0, 0);
+
+  // PV over 8 steps (t, u) of 16 keys.  Pinned order: under each of a step's 4 MFMAs, the
+  // 2 transpose reads and about a quarter of the exp/convert/sum work of the next step,
+  // so the matrix core, the LDS pipe and the VALU all stay busy.  Raised issue priority
+  // over this loop: the other wave on the SIMD (another work-group) fills the leftover
+  // VALU slots with its own softmax instead of competing for MFMA issue.
+  __builtin_amdgcn_s_setprio(1);
+  {
+    u32x4 vr[2][DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) vr[0][dt] = vread(dt, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+    for (int step = 0; step < 8; ++step) {
+      const int t = step >> 1, u = step & 1;
+      const int nt = (step + 1) >> 1, nu = (step + 1) & 1;
+      if (step + 1 < 8) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) vr[(step + 1) & 1][dt] = vread(dt, nt, nu);
+        make_p(nt, nu);
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        o[dt] = mfma32x32x16<CT>(vr[step & 1][dt], p[t][u], o[dt]);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (step + 1 < 8) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+        }
+      }
+    }
+  }
+  l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+  __builtin_amdgcn_s_setprio(0);
+  drain_then_barrier();  // B2
+  after_b2();
+}
+
+// Everything the d128 kernels need to know about one (b, h, q-block) work item.  All values
+// are wave-uniform (scalar registers).
+struct D128Item {
+  int item, qb, cnt, ntot;
+  const char *qbase, *kbase, *vbase, *kdbase, *vdbase;
+  const SA_CONST int32_t* list;
+};
+
+__device__ __forceinline__ D128Item d128_item(const FwdArgs& a, int item) {
+  D128Item it;
+  it.item = item;
+  const int bh = item / a.nqb;
+  it.qb = item - bh * a.nqb;
+  const int b = bh / a.H, h = bh - b * a.H;
+  // The plan is read-only for the kernel's lifetime: read it through the constant
+  // address space so the list walk compiles to scalar loads and never enters the
+  // vector-memory counter the DMA waits rely on.
+  it.cnt = __builtin_amdgcn_readfirstlane(((const SA_CONST int32_t*)a.counts)[item]);
+  it.list = (const SA_CONST int32_t*)(a.idx + (int64_t)item * a.nkb);
+  // Compensation tiles: after its listed tiles, a q-block below comp_qblocks attends every
+  // 128-key tile of kd/vd (same row strides as k/v) with comp_bias added to its logits.
+  it.ntot = it.cnt + (it.qb < a.comp_qblocks ? (a.Nd + 127) >> 7 : 0);
+  it.qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * 2;
+  it.kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)h * a.ks[1]) * 2;
+  it.vbase = (const char*)a.v + ((int64_t)b * a.vs[0] + (int64_t)h * a.vs[1]) * 2;
+  it.kdbase = (const char*)a.kd + ((int64_t)b * a.kds[0] + (int64_t)h * a.kds[1]) * 2;
+  it.vdbase = (const char*)a.vd + ((int64_t)b * a.vds[0] + (int64_t)h * a.vds[1]) * 2;
+  return it;
+}
+
+// Tile `t` of an item's walk: first key, valid key count, whether it is a compensation tile.
+__device__ __forceinline__ int d128_key0(const D128Item& it, int t) {
+  return t < it.cnt ? it.list[t] * 128 : (t - it.cnt) * 128;
+}
+__device__ __forceinline__ int d128_limit(const FwdArgs& a, const D128Item& it, int t) {
+  return t < it.cnt ? a.Nk : a.Nd;
+}
+
+template <int CT>
+__device__ __forceinline__ void d128_issue_k(const FwdArgs& a, const D128Item& it, int t, SA_LDS char* lk,
+                                             const D128Lanes& L, uint32_t kstride, int wave) {
+  const int key0 = d128_key0(it, t);
+  const char* base = (t < it.cnt ? it.kbase : it.kdbase) + (int64_t)key0 * kstride;
+  d128_copy_tile(lk, base, kstride, d128_limit(a, it, t) - key0, L.k_off, wave);
+}
+template <int CT>
+__device__ __forceinline__ void d128_issue_v(const FwdArgs& a, const D128Item& it, int t, SA_LDS char* lv,
+                                             const D128Lanes& L, uint32_t vstride, int wave) {
+  const int key0 = d128_key0(it, t);
+  const char* base = (t < it.cnt ? it.vbase : it.vdbase) + (int64_t)key0 * vstride;
+  d128_copy_tile(lv, base, vstride, d128_limit(a, it, t) - key0, L.v_off, wave);
+}
+
+// O of this wave's 32 rows through its 8 KB of an idle LDS tile buffer: each lane holds
+// 4-value pieces of its own row, so after the transpose every store instruction writes 4
+// whole 256-byte rows.  The caller guarantees that no wave reads the buffer and no copy
+// into it is in flight; each wave touches only its own slice.
+template <int CT>
+__device__ __forceinline__ void d128_store_o_staged(const FwdArgs& a, const D128Item& it, const f32x16 (&o)[4],
+                                                    float m_run, float l_run, SA_LDS char* buf, int wave,
+                                                    int lane) {
+  const int hl = lane >> 5, l32 = lane & 31;
+  const float l = sum_xor32(l_run);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  SA_LDS char* ob = buf + wave * 8192;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int chunk = (dt * 4 + g) ^ (l32 & 15);
+      u32x2 w;
+      w[0] = pack2<CT>(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv);
+      w[1] = pack2<CT>(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+      *(SA_LDS u32x2*)(ob + l32 * 256 + chunk * 16 + hl * 8) = w;
+    }
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0) only
+  const int bh = it.item / a.nqb;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int q0 = it.qb * 128 + wave * 32;
+  char* obase = (char*)a.out + ((int64_t)b * a.os[0] + (int64_t)h * a.os[1]) * 2;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int rr = 4 * i + (lane >> 4), cc = lane & 15;
+    const u32x4 val = *(SA_LDS const u32x4*)(ob + rr * 256 + ((cc ^ (rr & 15)) * 16));
+    if (q0 + rr < a.Nq)
+      *reinterpret_cast<u32x4*>(obase + ((int64_t)(q0 + rr) * a.os[2]) * 2 + cc * 16) = val;
+  }
+  const int qrow = q0 + l32;
+  if (qrow < a.Nq && a.lse != nullptr && hl == 0)
+    a.lse[((int64_t)b * a.H + h) * a.Nq + qrow] = it.ntot > 0 ? (m_run + __log2f(l)) * kLn2 : pos_inf();
+}
+
+// ------------------------------------------------------------------------------------
+// The per-q-block form: one work-group per order slot (or per row without an order).
+// ------------------------------------------------------------------------------------
 template <int CT>
 __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a) {
-  constexpr int DS = 8, DT = 4;
   __shared__ u32x4 lds_k[2048];
   __shared__ u32x4 lds_v[2048];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, l32 = lane & 31;
-  // Work-item values are uniform: keep them in scalar registers so the list walk uses
-  // scalar loads and never enters the vector-memory counter the DMA waits rely on.
   const int item = __builtin_amdgcn_readfirstlane(a.order ? a.order[blockIdx.x] : (int)blockIdx.x);
   if (item < 0) return;
-  const int bh = item / a.nqb;
-  const int qb = item - bh * a.nqb;
-  const int b = bh / a.H, h = bh - b * a.H;
-  const int cnt = __builtin_amdgcn_readfirstlane(a.counts[item]);
-  // The plan is read-only for the kernel's lifetime: read it through the constant
-  // address space so the list walk compiles to scalar loads.
-  const SA_CONST int32_t* list = (const SA_CONST int32_t*)(a.idx + (int64_t)item * a.nkb);
-  // Compensation tiles: after its listed tiles, a q-block below comp_qblocks attends every
-  // 128-key tile of kd/vd (same row strides as k/v) with comp_bias added to its logits.
-  const int ntot = cnt + (qb < a.comp_qblocks ? (a.Nd + 127) >> 7 : 0);
-
-  const char* qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * 2;
-  const char* kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)h * a.ks[1]) * 2;
-  const char* vbase = (const char*)a.v + ((int64_t)b * a.vs[0] + (int64_t)h * a.vs[1]) * 2;
-  const char* kdbase = (const char*)a.kd + ((int64_t)b * a.kds[0] + (int64_t)h * a.kds[1]) * 2;
-  const char* vdbase = (const char*)a.vd + ((int64_t)b * a.vds[0] + (int64_t)h * a.vds[1]) * 2;
+  const D128Item it = d128_item(a, item);
   const uint32_t kstride = (uint32_t)a.ks[2] * 2, vstride = (uint32_t)a.vs[2] * 2;
-  // Tile `it` of the walk: first key, valid key count, and whether it is a compensation tile.
-  auto tile_key0 = [&](int it) { return it < cnt ? list[it] * 128 : (it - cnt) * 128; };
-  auto tile_limit = [&](int it) { return it < cnt ? a.Nk : a.Nd; };
-
-  const int qrow = qb * 128 + wave * 32 + l32;
-  u32x4 qf[DS];
-  load_q_operand<CT, CT, 128>(qf, qbase, a.qs[2], qrow, a.Nq, hl);
-
-  // DMA: instruction j of wave w fills tile rows 16j + 4w + lane/16 (LDS bytes
-  // [(256j + 64w) * 16, +1024)); the swizzle of those rows does not depend on j.
-  const int drow = 4 * wave + (lane >> 4);
-  const uint32_t k_off = (uint32_t)drow * kstride + (uint32_t)(((lane & 15) ^ (drow & 15)) * 16);
-  const uint32_t v_off = (uint32_t)drow * vstride + (uint32_t)(((lane & 15) ^ (4 * (drow & 3))) * 16);
-  // LDS read addresses (bytes).  K: MFMA row t*32 + k_row_perm(l32), chunk 2ds + hl.
-  const int prow = k_row_perm(l32);
-  uint32_t ka[DS];
-#pragma unroll
-  for (int ds = 0; ds < DS; ++ds) ka[ds] = (uint32_t)(prow * 256 + (((2 * ds + hl) ^ (prow & 15)) * 16));
-  // V^T via transpose reads: 16-lane group g, lane s in group -> source row
-  // 8*(g/2) + 4r + s/4 (+16u + 32t), columns dt*32 + 16*(g%2) + 4*(s%4) .. +3.
-  uint32_t va[DT][2];
-  {
-    const int g = lane >> 4, sl = lane & 15;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int row = 8 * (g >> 1) + 4 * r + (sl >> 2);
-        const int chunk = dt * 4 + 2 * (g & 1) + ((sl & 3) >> 1);
-        const int phys = chunk ^ (4 * (row & 3));
-        va[dt][r] = (uint32_t)(row * 256 + phys * 16 + (sl & 1) * 8);
-      }
-  }
+  const D128Lanes L = d128_lanes(wave, lane, kstride, vstride);
   SA_LDS char* lk = (SA_LDS char*)lds_k;
   SA_LDS char* lv = (SA_LDS char*)lds_v;
 
-  auto issue_k = [&](int it) {
-    const int key0 = tile_key0(it);
-    const char* base = (it < cnt ? kbase : kdbase) + (int64_t)key0 * kstride;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(tile_limit(it) - key0) * kstride);
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      dma16(rs, (SA_LDS void*)(lk + (256 * j + 64 * wave) * 16), k_off + (uint32_t)j * 16u * kstride);
-  };
-  auto issue_v = [&](int it) {
-    const int key0 = tile_key0(it);
-    const char* base = (it < cnt ? vbase : vdbase) + (int64_t)key0 * vstride;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(tile_limit(it) - key0) * vstride);
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      dma16(rs, (SA_LDS void*)(lv + (256 * j + 64 * wave) * 16), v_off + (uint32_t)j * 16u * vstride);
-  };
+  const int qrow = it.qb * 128 + wave * 32 + l32;
+  u32x4 qf[8];
+  load_q_operand<CT, CT, 128>(qf, it.qbase, a.qs[2], qrow, a.Nq, hl);
 
-  f32x16 o[DT];
+  f32x16 o[4];
 #pragma unroll
-  for (int i = 0; i < DT; ++i) o[i] = f32x16{};
+  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
   float m_run = neg_inf();
   float l_run = 0.f;
   const float c = a.scale * kLog2e;
 
-  // Two barriers per tile.  B1 (after S): every wave is done reading K(it) and V(it)
-  // has landed -> K(it+1) may stream in.  B2 (after PV): every wave is done reading V(it)
-  // and K(it+1) has landed -> V(it+1) may stream in.
-  if (ntot > 0) {
-    issue_k(0);
-    issue_v(0);
+  if (it.ntot > 0) {
+    d128_issue_k<CT>(a, it, 0, lk, L, kstride, wave);
+    d128_issue_v<CT>(a, it, 0, lv, L, vstride, wave);
     // Drain both: waiting only for K(0) here leaves the compiler unable to prove at the
     // loop head that V's copies do not alias the K reads, and it then waits there on
     // every tile.
     drain_then_barrier();
   }
-  for (int it = 0; it < ntot; ++it) {
-    const int key0 = tile_key0(it);
-    const int klim = tile_limit(it);
-    const float bias = it < cnt ? 0.f : a.comp_bias;
-    const bool next = it + 1 < ntot;
-    f32x16 s[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) s[t] = f32x16{};
-    {
-      // Reads for k-step ds+1 are issued between the MFMAs of k-step ds, one read after
-      // each MFMA; the scheduling groups pin that order so no MFMA waits on the read
-      // issued just before it.
-      u32x4 kr[2][4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) kr[0][t] = *(SA_LDS const u32x4*)(lk + ka[0] + t * 8192);
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          s[t] = mfma32x32x16<CT>(kr[ds & 1][t], qf[ds], s[t]);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          if (ds + 1 < DS) {
-            kr[(ds + 1) & 1][t] = *(SA_LDS const u32x4*)(lk + ka[ds + 1] + t * 8192);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          }
-        }
-      }
-    }
-    drain_then_barrier();  // B1: V(it) has landed, K(it) reads are done
-    if (next) issue_k(it + 1);
-
-    if (key0 + 128 > klim) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (key0 + t * 32 + tile_key(hl, j) >= klim) s[t][j] = neg_inf();
-    }
-    float mx = neg_inf();
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
-    mx = max_xor32(mx);
-    // Lazy rescale: the reference point m_run moves only when this tile's maximum exceeds
-    // it by more than kLazyRescaleLog2, so P = exp2(c*s + bias - m_run) stays at most 2^8
-    // (well inside the range of bf16/f16 P and fp32 O, l) and the 64 multiplies of O run
-    // on few tiles.  O / l and m_run + log2(l) do not depend on the reference point.
-    const float m_tile = __builtin_fmaf(mx, c, bias);
-    if (m_tile > m_run + kLazyRescaleLog2) {
-      const float alpha = fast_exp2(m_run - m_tile);
-      l_run *= alpha;
-#pragma unroll
-      for (int i = 0; i < DT; ++i) o[i] *= alpha;
-      m_run = m_tile;
-    }
-    // P in the MFMA's 16-bit type; the row sum adds those rounded values (one dot2 per
-    // pair, four independent partial sums), so O and l are normalised by the same weights.
-    u32x4 p[4][2];
-    float lsum[4] = {0.f, 0.f, 0.f, 0.f};
-    auto make_p = [&](int t, int u) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float v0 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e], c, bias - m_run));
-        const float v1 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e + 1], c, bias - m_run));
-        p[t][u][e] = pack2<CT>(v0, v1);
-        lsum[t] = sum2_acc<CT>(p[t][u][e], lsum[t]);
-      }
-    };
-    // V^T operand for d-tile dt of step (t, u): two transpose reads.
-    auto vread = [&](int dt, int t, int u) -> u32x4 {
-      const uint32_t off = t * 8192 + u * 4096;
-      const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][0] + off));
-      const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + va[dt][1] + off));
-      const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
-      return u32x4{y0[0], y0[1], y1[0], y1[1]};
-    };
-    make_p(0, 0);
-
-    // PV over 8 steps (t, u) of 16 keys.  Pinned order: under each of a step's 4 MFMAs, the
-    // 2 transpose reads and about a quarter of the exp/convert/sum work of the next step,
-    // so the matrix core, the LDS pipe and the VALU all stay busy.  Raised issue priority
-    // over this loop: the other wave on the SIMD (another work-group) fills the leftover
-    // VALU slots with its own softmax instead of competing for MFMA issue.
-    __builtin_amdgcn_s_setprio(1);
-    {
-      u32x4 vr[2][DT];
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) vr[0][dt] = vread(dt, 0, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-      for (int step = 0; step < 8; ++step) {
-        const int t = step >> 1, u = step & 1;
-        const int nt = (step + 1) >> 1, nu = (step + 1) & 1;
-        if (step + 1 < 8) {
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) vr[(step + 1) & 1][dt] = vread(dt, nt, nu);
-          make_p(nt, nu);
-        }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          o[dt] = mfma32x32x16<CT>(vr[step & 1][dt], p[t][u], o[dt]);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          if (step + 1 < 8) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-          }
-        }
-      }
-    }
-    l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
-    __builtin_amdgcn_s_setprio(0);
-    drain_then_barrier();  // B2: K(it+1) has landed, V(it) reads are done
-    if (next) issue_v(it + 1);
+  for (int t = 0; t < it.ntot; ++t) {
+    const bool next = t + 1 < it.ntot;
+    d128_tile<CT>(lk, lv, L, qf, d128_key0(it, t), d128_limit(a, it, t), t < it.cnt ? 0.f : a.comp_bias,
+                  c, hl, o, m_run, l_run,
+                  [&] { if (next) d128_issue_k<CT>(a, it, t + 1, lk, L, kstride, wave); },
+                  [&] { if (next) d128_issue_v<CT>(a, it, t + 1, lv, L, vstride, wave); });
   }
 
-  const float l = sum_xor32(l_run);
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  // O goes out through this wave's 8 KB of the (now idle) K buffer: each lane holds 4-value
-  // pieces of its own row, so direct stores would be 32 partial rows per instruction; after
-  // the transpose every store instruction writes 4 whole 256-byte rows.  Every wave has
-  // passed the last barrier (no wave still reads K, no copy into it is in flight), and
-  // each wave touches only its own slice.
-  {
-    SA_LDS char* ob = lk + wave * 8192;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int chunk = (dt * 4 + g) ^ (l32 & 15);
-        u32x2 w;
-        w[0] = pack2<CT>(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv);
-        w[1] = pack2<CT>(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
-        *(SA_LDS u32x2*)(ob + l32 * 256 + chunk * 16 + hl * 8) = w;
-      }
-    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0) only
-    const int q0 = qb * 128 + wave * 32;
-    char* obase = (char*)a.out + ((int64_t)b * a.os[0] + (int64_t)h * a.os[1]) * 2;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int rr = 4 * i + (lane >> 4), c = lane & 15;
-      const u32x4 val = *(SA_LDS const u32x4*)(ob + rr * 256 + ((c ^ (rr & 15)) * 16));
-      if (q0 + rr < a.Nq)
-        *reinterpret_cast<u32x4*>(obase + ((int64_t)(q0 + rr) * a.os[2]) * 2 + c * 16) = val;
-    }
-  }
-  if (qrow < a.Nq && a.lse != nullptr && hl == 0)
-    a.lse[((int64_t)b * a.H + h) * a.Nq + qrow] = ntot > 0 ? (m_run + __log2f(l)) * kLn2 : pos_inf();
+  // O through this wave's 8 KB of the K buffer: every wave has passed the last barrier, so
+  // no wave still reads K and no copy into it is in flight.
+  d128_store_o_staged<CT>(a, it, o, m_run, l_run, lk, wave, lane);
 }
 
 // fp32 operands: every value is split as x = hi + lo with hi = bf16(x) and
