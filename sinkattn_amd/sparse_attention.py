@@ -23,7 +23,7 @@ import os
 import weakref
 from dataclasses import asdict, dataclass
 from pathlib import Path
-from typing import Dict, Iterable, Optional, Tuple
+from typing import Dict, Iterable, List, Optional, Sequence, Tuple
 
 import torch
 import torch.nn.functional as F
@@ -209,12 +209,9 @@ def _gpu_device_for(t: torch.Tensor) -> torch.device:
     return torch.device("cuda", torch.cuda.current_device())
 
 
-def _build_direct_mean_coverage_mask(mean_scores: torch.Tensor,
-                                     config: SinkSparseConfig) -> torch.Tensor:
-    """Per (head, q-block) row, keep the top key blocks until their mean mass reaches
-    ``offline_direct_coverage`` of the row, plus required blocks and the diagonal
-    (sparse_attention.py:268-376).  Runs the coverage_mask kernel; the result is a bool
-    tensor on ``mean_scores``' device, bit-identical to the reference's CPU result."""
+def _coverage_mask_args(mean_scores: torch.Tensor, config: SinkSparseConfig) -> tuple:
+    """Checks the [heads, blocks_q, blocks_k] shape; returns the kernel's (coverage,
+    keep_diagonal, required rows, required columns, video_residual text blocks or None)."""
     if mean_scores.dim() != 3:
         raise ValueError(f"Expected [heads, blocks_q, blocks_k] scores, got {tuple(mean_scores.shape)}")
     _, nq, nk = (int(x) for x in mean_scores.shape)
@@ -227,10 +224,57 @@ def _build_direct_mean_coverage_mask(mean_scores: torch.Tensor,
         tb = min(_ceil_div(int(config.text_length), int(config.block_size)), nq, nk)
         if tb > 0:
             video_tb = tb
+    return coverage, bool(config.keep_diagonal), rq, rk, video_tb
+
+
+def _build_direct_mean_coverage_mask(mean_scores: torch.Tensor,
+                                     config: SinkSparseConfig) -> torch.Tensor:
+    """Per (head, q-block) row, keep the top key blocks until their mean mass reaches
+    ``offline_direct_coverage`` of the row, plus required blocks and the diagonal
+    (sparse_attention.py:268-376).  Runs the coverage_mask kernel; the result is a bool
+    tensor on ``mean_scores``' device, bit-identical to the reference's CPU result."""
+    args = _coverage_mask_args(mean_scores, config)
     dev = _gpu_device_for(mean_scores)
     scores = mean_scores.float().to(dev)
-    mask = ops.coverage_mask(scores, coverage, bool(config.keep_diagonal), rq, rk, video_tb)
+    mask = ops.coverage_mask(scores, *args)
     return mask.to(mean_scores.device)
+
+
+def _build_direct_mean_coverage_masks(means: Sequence[torch.Tensor],
+                                      config: SinkSparseConfig) -> List[torch.Tensor]:
+    """`_build_direct_mean_coverage_mask` of every tensor of `means` (each its own call, its
+    own empty-row fallback included), with the host<->device traffic batched: equal-shaped
+    inputs go to the GPU in one copy, the kernels run back to back, and the masks come back
+    in one copy.  Results are on the inputs' device, as for the single call."""
+    if not means:
+        return []
+    args = [_coverage_mask_args(m, config) for m in means]
+    dev = _gpu_device_for(means[0])
+    home = means[0].device
+    if any(m.shape != means[0].shape or m.device != home for m in means):
+        return [_build_direct_mean_coverage_mask(m, config) for m in means]
+    scores = torch.stack([m.float() for m in means]).to(dev)
+    masks = torch.stack([ops.coverage_mask(scores[i], *args[i]) for i in range(len(means))])
+    return list(masks.to(home).unbind(0))
+
+
+def _to_host(tensors: Sequence[torch.Tensor], chunk_bytes: int = 256 << 20) -> List[torch.Tensor]:
+    """Host copies of equal-shaped tensors, stacked on their device in chunks of at most
+    `chunk_bytes` so that one copy moves many of them (the values are untouched)."""
+    out: List[torch.Tensor] = []
+    i = 0
+    while i < len(tensors):
+        t0 = tensors[i]
+        per = max(1, chunk_bytes // max(1, t0.numel() * t0.element_size()))
+        group = [t0]
+        while (i + len(group) < len(tensors) and len(group) < per
+               and tensors[i + len(group)].shape == t0.shape
+               and tensors[i + len(group)].dtype == t0.dtype
+               and tensors[i + len(group)].device == t0.device):
+            group.append(tensors[i + len(group)])
+        out.extend(torch.stack(group).cpu().unbind(0))
+        i += len(group)
+    return out
 
 
 # --- runtime statistics ----------------------------------------------------------------------
@@ -392,18 +436,24 @@ class SinkMaskCalibrator:
     def _build_mean_and_masks(self, config: Optional[SinkSparseConfig] = None) -> tuple[dict, dict, dict, dict]:
         config = self.config if config is None else config
         mean_scores, std_scores, sink_masks, counts = {}, {}, {}, {}
-        for layer_idx in sorted(self.score_sums):
+        layers = sorted(self.score_sums)
+        # every layer's sums come to the host in a few batched copies (not one sync per layer)
+        sums = _to_host([self.score_sums[i] for i in layers])
+        sq_sums = _to_host([self.score_sq_sums[i] for i in layers])
+        for j, layer_idx in enumerate(layers):
             key = str(layer_idx)
             n = self.score_counts[layer_idx]
             # the divisions on the host, as the reference does them (a GPU tensor / scalar
             # division is a multiply by the reciprocal, which can differ in the last bit)
-            mean = self.score_sums[layer_idx].cpu() / n
-            second = self.score_sq_sums[layer_idx].cpu() / n
+            mean = sums[j] / n
+            second = sq_sums[j] / n
             std = torch.sqrt((second - mean.square()).clamp_min_(0.0))
             mean_scores[key] = mean
             std_scores[key] = std
-            sink_masks[key] = _build_direct_mean_coverage_mask(mean, config).cpu()
             counts[key] = int(n)
+        masks = _build_direct_mean_coverage_masks([mean_scores[str(i)] for i in layers], config)
+        for layer_idx, m in zip(layers, masks):
+            sink_masks[str(layer_idx)] = m.cpu()
         return mean_scores, std_scores, sink_masks, counts
 
     @torch.no_grad()

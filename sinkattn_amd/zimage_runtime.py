@@ -28,6 +28,7 @@ from .sparse_attention import (
     _block_sparse_attn,
     _block_sparse_attn_with_compensation,
     _build_direct_mean_coverage_mask,
+    _build_direct_mean_coverage_masks,
     _ceil_div,
     _compute_block_scores,
     _dense_short_attention_with_lse,
@@ -35,6 +36,7 @@ from .sparse_attention import (
     _fused_compensation_supported,
     _mean_pool_sequence,
     _mix_attention_outputs,
+    _to_host,
     load_sink_mask_package,
 )
 
@@ -318,16 +320,22 @@ class ZImageSinkMaskCalibrator:
     def build_package(self, include_scores: bool = True, config_override: Optional[SinkSparseConfig] = None) -> dict:
         cfg = self.config if config_override is None else build_zimg_sink_config(package_config=asdict(config_override))
         means, stds, masks, counts = {}, {}, {}, {}
-        for layer in sorted(self.score_sums):
+        layers = sorted(self.score_sums)
+        # finished on the host like the reference; the sums of all layers come over in a
+        # few batched copies and the masks are built back to back on the GPU
+        pres = _to_host([self.score_presence_sums[i] for i in layers])
+        sums = _to_host([self.score_sums[i] for i in layers])
+        sq_sums = _to_host([self.score_sq_sums[i] for i in layers])
+        for j, layer in enumerate(layers):
             key = str(layer)
-            # finished on the host like the reference (one copy of the sums per layer)
-            presence = self.score_presence_sums[layer].cpu().clamp_min_(1.0)
-            mean = self.score_sums[layer].cpu() / presence
-            var = (self.score_sq_sums[layer].cpu() / presence - mean.square()).clamp_min_(0.0)
-            masks[key] = _build_direct_mean_coverage_mask(mean, cfg).cpu()
+            presence = pres[j].clamp_min(1.0)
+            mean = sums[j] / presence
+            var = (sq_sums[j] / presence - mean.square()).clamp_min_(0.0)
             means[key] = mean
             stds[key] = torch.sqrt(var)
             counts[key] = int(self.score_counts[layer])
+        for layer, m in zip(layers, _build_direct_mean_coverage_masks([means[str(i)] for i in layers], cfg)):
+            masks[str(layer)] = m.cpu()
         return {
             "version": 3,
             "config": asdict(cfg),

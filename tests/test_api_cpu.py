@@ -200,8 +200,8 @@ def test_calibrator_accumulation_math(monkeypatch):
     it = iter(seq)
     monkeypatch.setattr(sa, "_compute_block_scores", lambda q, k, v, c: next(it))
     captured = {}
-    monkeypatch.setattr(sa, "_build_direct_mean_coverage_mask",
-                        lambda mean, cfg: captured.setdefault("m", torch_ref.coverage_mask(mean)))
+    monkeypatch.setattr(sa, "_build_direct_mean_coverage_masks",
+                        lambda means, cfg: [captured.setdefault("m", torch_ref.coverage_mask(m)) for m in means])
     cal = sa.SinkMaskCalibrator(sa.SinkSparseConfig())
     for _ in range(3):
         cal.record(0, None, None, None)
