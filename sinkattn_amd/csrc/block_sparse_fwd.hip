@@ -692,11 +692,16 @@ __global__ __launch_bounds__(256) void plan_rows_kernel(PlanArgs a) {
 // chunks per head).  When the chunk count is not a multiple of 8, the heads of the last,
 // partial round are cut finer (C * F chunks each, F = 8 / gcd(their chunks, 8)), so that
 // every XCD can get the same share of them.  Whole chunks, then the fine chunks, are dealt
-// to the 8 XCDs longest-processing-time first (cost = listed tiles + one per q-block), each
+// to the 8 XCDs longest-processing-time first (cost = listed tiles + kQblockCost per q-block), each
 // kind at most ceil(count / 8) per XCD, so every XCD gets nearly the same work whatever the
 // per-head densities; an XCD runs its whole chunks, then its fine chunks, each kind in
 // (head, j) order, and a chunk's q-blocks longest first.  Slots past the end of a shorter
 // chunk hold -1.
+// Fixed cost of a q-block in the launch-order model, in tiles: a work-group's start (order
+// entry, count and list reads), its first K/V copies and its O stores take about as long as
+// two tiles (per work-group timestamps at the Z-Image layer: 7.3 us per q-block + 3.45 us
+// per tile).
+constexpr int kQblockCost = 2;
 constexpr int kChunkQb = 128;
 constexpr int kMaxChunks = 4096;
 constexpr int kMaxOutliers = 1024;
@@ -793,7 +798,7 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
     int bh, j, C;
     chunk_head(ch, bh, j, C);
     int w = 0;
-    for (int qb = j; qb < a.nqb; qb += C) w += counts(bh * a.nqb + qb) + 1;
+    for (int qb = j; qb < a.nqb; qb += C) w += counts(bh * a.nqb + qb) + kQblockCost;
     cost[ch] = w;
   }
   __syncthreads();
@@ -857,13 +862,13 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
   for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
     int C, j;
     const int x = xcd[chunk_of(row, C, j)];
-    atomicAdd(&xsum[x], counts(row) + 1);
+    atomicAdd(&xsum[x], counts(row) + kQblockCost);
     atomicAdd(&xcnt[x], 1);
   }
   __syncthreads();
-  // a q-block of `c` tiles on XCD x is an outlier when (c + 1) * count > 2 * sum
+  // a q-block of `c` tiles on XCD x is an outlier when (c + kQblockCost) * count > 2 * sum
   auto above = [&](int c, int x) __attribute__((always_inline)) {
-    return (int64_t)(c + 1) * xcnt[x] > 2 * (int64_t)xsum[x];
+    return (int64_t)(c + kQblockCost) * xcnt[x] > 2 * (int64_t)xsum[x];
   };
   for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
     int C, j;
@@ -890,7 +895,7 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
     const int64_t xc = xcnt[xcd[ch]], xs2 = 2 * (int64_t)xsum[xcd[ch]];
     int n = 0;
     for (int qb = j; qb < a.nqb; qb += C)
-      n += !(use_out && (int64_t)(counts(bh * a.nqb + qb) + 1) * xc > xs2);
+      n += !(use_out && (int64_t)(counts(bh * a.nqb + qb) + kQblockCost) * xc > xs2);
     nonout[ch] = (int16_t)n;
   }
   __syncthreads();
@@ -939,7 +944,7 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
         key[u] = -1;
         if (k < S) {
           const int c = counts(bh * a.nqb + j + k * C);
-          if ((int64_t)(c + 1) * xc <= xs2) key[u] = c * 256 + (255 - k);
+          if ((int64_t)(c + kQblockCost) * xc <= xs2) key[u] = c * 256 + (255 - k);
         }
         keys[k] = key[u];
       }

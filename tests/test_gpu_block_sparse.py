@@ -208,13 +208,14 @@ def _chunk_layout(nbh, nqb):
 
 
 MAX_OUTLIERS = 1024  # q-blocks taken out of the chunk sequences, in the whole plan
+QBLOCK_COST = 2      # fixed cost of a q-block in the launch-order model, in tiles
 
 
 def _check_order(plan, counts, nbh, nqb):
     """Launch-order invariants: a permutation of the rows; slot i runs on XCD i % 8; every
     chunk (q-blocks qb = j mod C of one head) on one XCD, at most ceil(n / 8) chunks of each
     kind (whole, fine) per XCD; each XCD's slots hold, from slot 0: its outliers (cost =
-    tiles + 1 above twice the XCD's mean; none when the plan has more than MAX_OUTLIERS) by
+    tiles + QBLOCK_COST above twice the XCD's mean; none when the plan has more than MAX_OUTLIERS) by
     cost desc, then its fine chunks, then its whole chunks (each kind in ascending chunk
     order), each chunk's other q-blocks by cost desc; LPT keeps the XCD loads within one
     chunk's cost."""
@@ -232,7 +233,7 @@ def _check_order(plan, counts, nbh, nqb):
             return bh * L["Cw"] + qb % L["Cw"]
         return L["nw"] + (bh - L["nbh_w"]) * L["Cs"] + qb % L["Cs"]
 
-    cost = [int(counts[r]) + 1 for r in range(rows)]
+    cost = [int(counts[r]) + QBLOCK_COST for r in range(rows)]
     chunk_xcd = {}
     for i, r in enumerate(order):
         if r >= 0:
