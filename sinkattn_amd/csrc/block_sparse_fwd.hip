@@ -369,27 +369,27 @@ __device__ __forceinline__ D128Item d128_item(const FwdArgs& a, int item) {
   return it;
 }
 
-// Tile `t` of an item's walk: first key, valid key count, whether it is a compensation tile.
+// Tile `t` of an item's walk (listed tiles, then compensation tiles): its first key.  The
+// list entry is read unconditionally at an index clamped into the row's own list, so that the
+// load can be issued a whole tile before it is needed without ever leaving the plan.
 __device__ __forceinline__ int d128_key0(const D128Item& it, int t) {
-  return t < it.cnt ? it.list[t] * 128 : (t - it.cnt) * 128;
-}
-__device__ __forceinline__ int d128_limit(const FwdArgs& a, const D128Item& it, int t) {
-  return t < it.cnt ? a.Nk : a.Nd;
+  const int e = it.list[t < it.cnt ? t : (it.cnt > 0 ? it.cnt - 1 : 0)];
+  return t < it.cnt ? e * 128 : (t - it.cnt) * 128;
 }
 
+// K (or V) rows [key0, key0 + 128) of the listed keys (comp = false) or of the pooled keys
+// (comp = true); rows at or past klim read as zero.
 template <int CT>
-__device__ __forceinline__ void d128_issue_k(const FwdArgs& a, const D128Item& it, int t, SA_LDS char* lk,
+__device__ __forceinline__ void d128_issue_k(const D128Item& it, int key0, int klim, bool comp, SA_LDS char* lk,
                                              const D128Lanes& L, uint32_t kstride, int wave) {
-  const int key0 = d128_key0(it, t);
-  const char* base = (t < it.cnt ? it.kbase : it.kdbase) + (int64_t)key0 * kstride;
-  d128_copy_tile(lk, base, kstride, d128_limit(a, it, t) - key0, L.k_off, wave);
+  const char* base = (comp ? it.kdbase : it.kbase) + (int64_t)key0 * kstride;
+  d128_copy_tile(lk, base, kstride, klim - key0, L.k_off, wave);
 }
 template <int CT>
-__device__ __forceinline__ void d128_issue_v(const FwdArgs& a, const D128Item& it, int t, SA_LDS char* lv,
+__device__ __forceinline__ void d128_issue_v(const D128Item& it, int key0, int klim, bool comp, SA_LDS char* lv,
                                              const D128Lanes& L, uint32_t vstride, int wave) {
-  const int key0 = d128_key0(it, t);
-  const char* base = (t < it.cnt ? it.vbase : it.vdbase) + (int64_t)key0 * vstride;
-  d128_copy_tile(lv, base, vstride, d128_limit(a, it, t) - key0, L.v_off, wave);
+  const char* base = (comp ? it.vdbase : it.vbase) + (int64_t)key0 * vstride;
+  d128_copy_tile(lv, base, vstride, klim - key0, L.v_off, wave);
 }
 
 // O of this wave's 32 rows through its 8 KB of an idle LDS tile buffer: each lane holds
@@ -461,9 +461,14 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
   float l_run = 0.f;
   const float c = a.scale * kLog2e;
 
+  // kernel arguments the tile loop needs, read once
+  const int Nk = a.Nk, Nd = a.Nd;
+  const float comp_bias = a.comp_bias;
+  int key0 = d128_key0(it, 0);
+  int klim = it.cnt > 0 ? Nk : Nd;
   if (it.ntot > 0) {
-    d128_issue_k<CT>(a, it, 0, lk, L, kstride, wave);
-    d128_issue_v<CT>(a, it, 0, lv, L, vstride, wave);
+    d128_issue_k<CT>(it, key0, klim, it.cnt == 0, lk, L, kstride, wave);
+    d128_issue_v<CT>(it, key0, klim, it.cnt == 0, lv, L, vstride, wave);
     // Drain both: waiting only for K(0) here leaves the compiler unable to prove at the
     // loop head that V's copies do not alias the K reads, and it then waits there on
     // every tile.
@@ -471,10 +476,16 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
   }
   for (int t = 0; t < it.ntot; ++t) {
     const bool next = t + 1 < it.ntot;
-    d128_tile<CT>(lk, lv, L, qf, d128_key0(it, t), d128_limit(a, it, t), t < it.cnt ? 0.f : a.comp_bias,
-                  c, hl, o, m_run, l_run,
-                  [&] { if (next) d128_issue_k<CT>(a, it, t + 1, lk, L, kstride, wave); },
-                  [&] { if (next) d128_issue_v<CT>(a, it, t + 1, lv, L, vstride, wave); });
+    const bool comp_next = t + 1 >= it.cnt;
+    // the next tile's first key: its list entry is loaded here, a whole S phase before the
+    // copies after B1 need it
+    const int key0_next = d128_key0(it, t + 1);
+    const int klim_next = comp_next ? Nd : Nk;
+    d128_tile<CT>(lk, lv, L, qf, key0, klim, t < it.cnt ? 0.f : comp_bias, c, hl, o, m_run, l_run,
+                  [&] { if (next) d128_issue_k<CT>(it, key0_next, klim_next, comp_next, lk, L, kstride, wave); },
+                  [&] { if (next) d128_issue_v<CT>(it, key0_next, klim_next, comp_next, lv, L, vstride, wave); });
+    key0 = key0_next;
+    klim = klim_next;
   }
 
   // O through this wave's 8 KB of the K buffer: every wave has passed the last barrier, so
