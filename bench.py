@@ -55,7 +55,7 @@ def _parse():
     p.add_argument("--no-extras", action="store_true", help="skip dense/pooling/mask timings")
     p.add_argument("--cpu-sample-qblocks", type=int, default=0,
                    help="q-blocks of the layer the CPU baseline times (0 = the whole layer, 6144)")
-    p.add_argument("--only", choices=["all", "fa", "pool", "maxpool", "mask"], default="all",
+    p.add_argument("--only", choices=["all", "fa", "fa4", "pool", "maxpool", "mask"], default="all",
                    help="profiling aid: run just one kernel family (no JSON line unless 'all')")
     p.add_argument("--copy-mb", type=int, default=0,
                    help="profiling aid: first run a device copy of this many MiB (counter calibration)")
@@ -208,8 +208,13 @@ def main():
     def kernel_call():
         ops.block_sparse_attention(q, k, v, plan, return_lse=True)
 
+    if args.only == "fa4":  # the config-4 (Z-Image) attention alone
+        del q, k, v
+        qz, kz, vz, _, _, mz = zimage_inputs(torch, dev, sa)
+        zplan = ops.block_sparse_plan(mz)
+        kernel_call = lambda: ops.block_sparse_attention(qz, kz, vz, zplan)  # noqa: E731
     if args.only != "all":
-        fn = {"fa": kernel_call, "pool": lambda: ops.block_mass_scores(q, k),
+        fn = {"fa": kernel_call, "fa4": kernel_call, "pool": lambda: ops.block_mass_scores(q, k),
               "maxpool": lambda: ops.max_pool_scores(q, k, 1.0 / math.sqrt(D)),
               "mask": lambda: ops.coverage_mask(torch.rand(H, 256, 256, device=dev), 0.85, True)}[args.only]
         for _ in range(args.warmup + args.steps):
@@ -355,21 +360,31 @@ def main():
     print(json.dumps(out))
 
 
-def zimage_layer(torch, dev, ops, sa, args):
-    """Z-Image-Turbo 2048x2048 layer (B=1, H=30, 16384 image + 512 text tokens, d=128 bf16,
-    text keys x4): exact pooling -> coverage-0.85 mask -> sparse attention with the text
-    rows and columns forced dense, as the Z-Image runtime runs it."""
+def zimage_inputs(torch, dev, sa):
+    """Z-Image-Turbo 2048x2048 layer inputs (B=1, H=30, 16384 image + 512 text tokens,
+    d=128 bf16, text keys x4), the runtime config, and the sparse mask the runtime runs:
+    exact pooling -> coverage-0.85 mask -> text rows and columns forced dense."""
     from sinkattn_amd import zimage_runtime as zr
     B, H, N, D = 1, 30, 16896, 128
     g = torch.Generator(device=dev).manual_seed(30)
     q, k, v = (torch.randn(B, H, N, D, device=dev, dtype=torch.bfloat16, generator=g) for _ in range(3))
     k[:, :, N - 512:] *= 4.0
-    cfg = zr.build_zimg_sink_config()
-    pms = time_fn(torch, lambda: sa._compute_block_scores(q, k, v, cfg), 3, 1)
+    # exact block mass: the Z-Image calibration CLI's default (zimg/offline/calibrate_sink_sparse.py:109)
+    cfg = zr.build_zimg_sink_config(config_overrides={"pooling_mode": "exact"})
     scores = sa._compute_block_scores(q, k, v, cfg).mean(0)
-    mus = time_fn(torch, lambda: sa._build_direct_mean_coverage_mask(scores, cfg), 10, 2) * 1e3
     mask = sa._build_direct_mean_coverage_mask(scores, cfg)
     mask = zr._force_text_dense_runtime_mask(mask, image_blocks=128, current_text_blocks=4)[None]
+    return q, k, v, cfg, scores, mask
+
+
+def zimage_layer(torch, dev, ops, sa, args):
+    """Z-Image-Turbo 2048x2048 layer (config 4): exact pooling -> coverage-0.85 mask ->
+    sparse attention with the text rows and columns forced dense, as the Z-Image runtime
+    runs it."""
+    q, k, v, cfg, scores, mask = zimage_inputs(torch, dev, sa)
+    B, H, N, D = (int(x) for x in q.shape)
+    pms = time_fn(torch, lambda: sa._compute_block_scores(q, k, v, cfg), 3, 1)
+    mus = time_fn(torch, lambda: sa._build_direct_mean_coverage_mask(scores, cfg), 10, 2) * 1e3
     plan = ops.block_sparse_plan(mask)
     dplan = ops.block_sparse_plan(torch.ones_like(mask))
     flops = tile_flops(torch, mask, N, N, D)
