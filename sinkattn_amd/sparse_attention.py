@@ -413,6 +413,14 @@ class SinkMaskCalibrator:
     and finishes there like the reference, so the package is bit-identical to host
     accumulation."""
 
+    # Where the per-layer sums live.  On the GPU (default) they cost 2 x 4 bytes x heads x
+    # q-blocks x k-blocks per layer of device memory for the whole calibration (Wan2.1-1.3B:
+    # 30 x 12 x 256 x 256 -> 189 MB; Wan2.1-14B at 720p: 40 x 40 x 591 x 591 -> 4.5 GB) and
+    # no host sync per call.  Set to True for the reference's behaviour: each call's batch
+    # mean is copied to the host (one sync per call) and accumulated there.  The package is
+    # bit-identical either way (the same fp32 adds and squares).
+    accumulate_on_host: bool = False
+
     def __init__(self, config: SinkSparseConfig):
         self.config = config
         self.current_step = -1
@@ -424,6 +432,8 @@ class SinkMaskCalibrator:
         self.current_step = -1
 
     def _accumulate_score(self, layer_idx: int, scores: torch.Tensor) -> None:
+        if self.accumulate_on_host:
+            scores = scores.cpu()
         if layer_idx not in self.score_sums:
             self.score_sums[layer_idx] = scores
             self.score_sq_sums[layer_idx] = scores.square()

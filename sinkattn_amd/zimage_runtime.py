@@ -279,7 +279,15 @@ class ZImageSinkMaskCalibrator:
     def reset_generation(self) -> None:
         self.current_step = -1
 
+    # The per-layer sums (and presence counts) stay on the scores' device unless this is set:
+    # 3 x 4 bytes x heads x blocks^2 per layer while calibrating; True copies each call's
+    # aligned scores to the host first, as the reference does (one sync per call).  The
+    # package is bit-identical either way.
+    accumulate_on_host: bool = False
+
     def _accumulate(self, *, layer_idx: int, scores: torch.Tensor, presence: torch.Tensor) -> None:
+        if self.accumulate_on_host:
+            scores, presence = scores.cpu(), presence.cpu()
         if layer_idx not in self.score_sums:
             self.score_sums[layer_idx] = scores
             self.score_sq_sums[layer_idx] = scores.square()

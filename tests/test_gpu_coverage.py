@@ -158,16 +158,22 @@ def test_calibrator_device_accumulation_is_bit_identical():
     torch.manual_seed(1)
     cfg = sa.SinkSparseConfig(pooling_mode="exact")
     cal = sa.SinkMaskCalibrator(cfg)
+    cal_host = sa.SinkMaskCalibrator(cfg)
+    cal_host.accumulate_on_host = True  # the reference's placement of the sums
     host_sum, host_sq = None, None
     for step in range(3):
         q = torch.randn(2, 2, 700, 128, device="cuda", dtype=torch.bfloat16)
         k = torch.randn(2, 2, 700, 128, device="cuda", dtype=torch.bfloat16)
         cal.record(0, q, k, k)
+        cal_host.record(0, q, k, k)
         m = sa._compute_block_scores(q, k, k, cfg).float().mean(dim=0).cpu()
         host_sum = m.clone() if host_sum is None else host_sum + m
         host_sq = m.square() if host_sq is None else host_sq + m.square()
-    assert cal.score_sums[0].is_cuda
+    assert cal.score_sums[0].is_cuda and cal_host.score_sums[0].device.type == "cpu"
     pkg = cal.build_package()
+    pkg_host = cal_host.build_package()
+    for part in ("mean_scores", "std_scores", "sink_masks"):
+        assert torch.equal(pkg[part]["0"], pkg_host[part]["0"]), part
     mean = host_sum / 3
     std = torch.sqrt((host_sq / 3 - mean.square()).clamp_min_(0.0))
     assert torch.equal(pkg["mean_scores"]["0"], mean)

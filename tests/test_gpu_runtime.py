@@ -252,6 +252,8 @@ def test_zimage_calibrator_vs_oracle():
     cfg = SinkSparseConfig(token_width=16, token_height=16, token_depth=1, text_length=256, pooling_mode="exact",
                            offline_direct_coverage=0.85)
     cal = zr.ZImageSinkMaskCalibrator(cfg)
+    cal_host = zr.ZImageSinkMaskCalibrator(cfg)
+    cal_host.accumulate_on_host = True  # the reference's placement of the sums
     it, ib, T = cal.image_token_count, cal.image_blocks, cal.total_blocks
     assert (it, ib, T) == (256, 2, 4)
     samples = []
@@ -260,8 +262,13 @@ def test_zimage_calibrator_vs_oracle():
         q, k = (torch.randn(1, H, n, D, device=DEV, dtype=torch.bfloat16) for _ in range(2))
         k[:, :, :3] *= 5.0
         cal.record(0, q, k, k, text_token_count=text)
+        cal_host.record(0, q, k, k, text_token_count=text)
         samples.append((q, k, text))
+    assert cal.score_sums[0].is_cuda and cal_host.score_sums[0].device.type == "cpu"
     pkg = cal.build_package()
+    pkg_host = cal_host.build_package()
+    for part in ("mean_scores", "std_scores", "sink_masks"):
+        assert torch.equal(pkg[part]["0"].cpu(), pkg_host[part]["0"].cpu()), part
     # oracle: exact mass per sample, aligned by explicit block copies, mean over presence
     sums = torch.zeros(H, T, T)
     pres = torch.zeros(H, T, T)
