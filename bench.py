@@ -49,7 +49,8 @@ def _parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=20,
+                   help="untimed calls before each timed loop (the first ~15 launches of a fresh process run up to 20%% slower while the GPU clock ramps)")
     p.add_argument("--density", type=float, default=0.20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true", help="skip dense/pooling/mask timings")
