@@ -174,6 +174,33 @@ def cpu_baseline(torch, q, k, v, mask, n_qblocks, total_flops_layer):
     }
 
 
+def cpu_calibration_baseline(torch, ops, q, k, gpu_pool_ms, gpu_mask_us):
+    """The calibration steps on the host, as the reference computes them (the oracle restates
+    its torch ops): the exact block mass of one (b, h) pair of the config-2 layer, scaled to
+    the layer's 24 pairs, and the coverage-0.85 mask of the layer's batch-mean map (the
+    reference builds that mask on the CPU)."""
+    from oracle import torch_ref
+
+    B, H = int(q.shape[0]), int(q.shape[1])
+    qs, ks = q[:1, :1].cpu(), k[:1, :1].cpu()
+    t0 = time.perf_counter()
+    torch_ref.exact_block_mass(qs, ks)
+    pool_s = time.perf_counter() - t0
+    mean_map = ops.block_mass_scores(q, k).mean(dim=0).cpu()
+    t0 = time.perf_counter()
+    torch_ref.coverage_mask(mean_map, coverage=0.85, keep_diagonal=True)
+    mask_s = time.perf_counter() - t0
+    return {
+        "pooling_ms_per_layer": round(pool_s * B * H * 1e3, 1),
+        "pooling_sample": (f"1 of {B * H} (b, h) pairs of the config-2 layer, fp32 exact block mass "
+                           f"(two passes over 16-block key chunks) on CPU, {pool_s:.1f} s, x{B * H}"),
+        "pooling_gpu_ms": round(gpu_pool_ms, 3),
+        "coverage_mask_ms": round(mask_s * 1e3, 1),
+        "coverage_mask_sample": f"the layer's [{H}, 256, 256] mean map, whole, torch sort + cumsum on CPU",
+        "coverage_mask_gpu_us": round(gpu_mask_us, 1),
+    }
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -358,6 +385,9 @@ def main():
 
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, q, k, v, mask, args.cpu_sample_qblocks, flops)
+        if "pooling" in out:
+            out["cpu_baseline"]["calibration"] = cpu_calibration_baseline(
+                torch, ops, q, k, out["pooling"]["ms"], out["coverage_mask_us"])
     print(json.dumps(out))
 
 
