@@ -300,13 +300,13 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
     const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
     return u32x4{y0[0], y0[1], y1[0], y1[1]};
   };
-  make_p(0, 0);
-
-  // PV over 8 steps (t, u) of 16 keys.  Pinned order: under each of a step's 4 MFMAs, the
-  // 2 transpose reads and about a quarter of the exp/convert/sum work of the next step,
-  // so the matrix core, the LDS pipe and the VALU all stay busy.  Raised issue priority
-  // over this loop: the other wave on the SIMD (another work-group) fills the leftover
-  // VALU slots with its own softmax instead of competing for MFMA issue.
+  // All of P first, then PV.  Each wave's tile then runs as three phases, S (MFMAs and K
+  // reads), softmax (VALU only) and PV (MFMAs and V^T transpose reads), and the VALU slots
+  // of S and PV stay free for the other work-group's wave on the SIMD, which is in another
+  // phase.  Interleaving the exps of later steps under the PV MFMAs (or the row max under S)
+  // measured slower.  Raised issue priority over PV.
+#pragma unroll
+  for (int step = 0; step < 8; ++step) make_p(step >> 1, step & 1);
   __builtin_amdgcn_s_setprio(1);
   {
     u32x4 vr[2][DT];
@@ -320,16 +320,13 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
       if (step + 1 < 8) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) vr[(step + 1) & 1][dt] = vread(dt, nt, nu);
-        make_p(nt, nu);
       }
+      // under each MFMA, two transpose reads of the next step
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         o[dt] = mfma32x32x16<CT>(vr[step & 1][dt], p[t][u], o[dt]);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (step + 1 < 8) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-        }
+        if (step + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
     }
   }
