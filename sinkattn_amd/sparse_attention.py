@@ -443,27 +443,53 @@ class SinkMaskCalibrator:
             self.score_sq_sums[layer_idx] += scores.square()
             self.score_counts[layer_idx] += 1
 
-    def _build_mean_and_masks(self, config: Optional[SinkSparseConfig] = None) -> tuple[dict, dict, dict, dict]:
+    def _build_mean_and_masks(self, config: Optional[SinkSparseConfig] = None, *,
+                              need_scores: bool = True) -> tuple[dict, dict, dict, dict]:
         config = self.config if config is None else config
         mean_scores, std_scores, sink_masks, counts = {}, {}, {}, {}
         layers = sorted(self.score_sums)
-        # every layer's sums come to the host in a few batched copies (not one sync per layer)
-        sums = _to_host([self.score_sums[i] for i in layers])
-        sq_sums = _to_host([self.score_sq_sums[i] for i in layers])
+        if not layers:
+            return mean_scores, std_scores, sink_masks, counts
+        first = self.score_sums[layers[0]]
+        on_device = first.is_cuda and all(self.score_sums[i].shape == first.shape
+                                          and self.score_sums[i].device == first.device for i in layers)
+        if on_device:
+            # Mean and std where the sums are, all layers at once.  The count is a device
+            # tensor, so the division is an elementwise IEEE division, as the reference's host
+            # division (a division by a Python number would be a multiply by its reciprocal).
+            sums = torch.stack([self.score_sums[i] for i in layers])
+            n = torch.tensor([float(self.score_counts[i]) for i in layers], device=first.device)
+            n = n.view(-1, *([1] * first.dim()))
+            mean = sums / n
+            del sums
+            masks = _build_direct_mean_coverage_masks(list(mean.unbind(0)), config)
+            # the package lives on the host: the masks always, the scores when asked for
+            masks = _to_host(masks)
+            means = stds = None
+            if need_scores:
+                var = (torch.stack([self.score_sq_sums[i] for i in layers]) / n - mean.square()).clamp_min_(0.0)
+                means = _to_host(list(mean.unbind(0)))
+                # the square root on the host: torch's device sqrt is not correctly rounded
+                stds = [torch.sqrt(x) for x in _to_host(list(var.unbind(0)))]
+        else:
+            # sums on the host (accumulate_on_host, or mixed shapes): the reference's host math
+            sums = _to_host([self.score_sums[i] for i in layers])
+            sq_sums = _to_host([self.score_sq_sums[i] for i in layers])
+            means, stds = [], []
+            for j, layer_idx in enumerate(layers):
+                n = self.score_counts[layer_idx]
+                mean = sums[j] / n
+                second = sq_sums[j] / n
+                means.append(mean)
+                stds.append(torch.sqrt((second - mean.square()).clamp_min_(0.0)))
+            masks = [m.cpu() for m in _build_direct_mean_coverage_masks(means, config)]
         for j, layer_idx in enumerate(layers):
             key = str(layer_idx)
-            n = self.score_counts[layer_idx]
-            # the divisions on the host, as the reference does them (a GPU tensor / scalar
-            # division is a multiply by the reciprocal, which can differ in the last bit)
-            mean = sums[j] / n
-            second = sq_sums[j] / n
-            std = torch.sqrt((second - mean.square()).clamp_min_(0.0))
-            mean_scores[key] = mean
-            std_scores[key] = std
-            counts[key] = int(n)
-        masks = _build_direct_mean_coverage_masks([mean_scores[str(i)] for i in layers], config)
-        for layer_idx, m in zip(layers, masks):
-            sink_masks[str(layer_idx)] = m.cpu()
+            if means is not None:
+                mean_scores[key] = means[j]
+                std_scores[key] = stds[j]
+            sink_masks[key] = masks[j]
+            counts[key] = int(self.score_counts[layer_idx])
         return mean_scores, std_scores, sink_masks, counts
 
     @torch.no_grad()
@@ -478,7 +504,8 @@ class SinkMaskCalibrator:
     def build_package(self, include_scores: bool = True,
                       config_override: Optional[SinkSparseConfig] = None) -> dict:
         cfg = self.config if config_override is None else config_override
-        mean_scores, std_scores, sink_masks, counts = self._build_mean_and_masks(config=cfg)
+        mean_scores, std_scores, sink_masks, counts = self._build_mean_and_masks(config=cfg,
+                                                                               need_scores=include_scores)
         return {
             "version": 3,
             "config": asdict(cfg),

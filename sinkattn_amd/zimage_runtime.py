@@ -329,21 +329,45 @@ class ZImageSinkMaskCalibrator:
         cfg = self.config if config_override is None else build_zimg_sink_config(package_config=asdict(config_override))
         means, stds, masks, counts = {}, {}, {}, {}
         layers = sorted(self.score_sums)
-        # finished on the host like the reference; the sums of all layers come over in a
-        # few batched copies and the masks are built back to back on the GPU
-        pres = _to_host([self.score_presence_sums[i] for i in layers])
-        sums = _to_host([self.score_sums[i] for i in layers])
-        sq_sums = _to_host([self.score_sq_sums[i] for i in layers])
-        for j, layer in enumerate(layers):
-            key = str(layer)
-            presence = pres[j].clamp_min(1.0)
-            mean = sums[j] / presence
-            var = (sq_sums[j] / presence - mean.square()).clamp_min_(0.0)
-            means[key] = mean
-            stds[key] = torch.sqrt(var)
-            counts[key] = int(self.score_counts[layer])
-        for layer, m in zip(layers, _build_direct_mean_coverage_masks([means[str(i)] for i in layers], cfg)):
-            masks[str(layer)] = m.cpu()
+        if not layers:
+            pass
+        elif all(self.score_sums[i].is_cuda for i in layers):
+            # mean and std on the device, all layers at once (elementwise IEEE divisions by the
+            # presence counts, as the reference's host math); the masks are built from the
+            # device means and only what the package holds comes to the host
+            sums = torch.stack([self.score_sums[i] for i in layers])
+            presence = torch.stack([self.score_presence_sums[i] for i in layers]).clamp_min_(1.0)
+            mean = sums / presence
+            del sums
+            mask_list = _to_host(_build_direct_mean_coverage_masks(list(mean.unbind(0)), cfg))
+            mean_list = std_list = None
+            if include_scores:
+                var = (torch.stack([self.score_sq_sums[i] for i in layers]) / presence - mean.square()).clamp_min_(0.0)
+                mean_list = _to_host(list(mean.unbind(0)))
+                # the square root on the host: torch's device sqrt is not correctly rounded
+                std_list = [torch.sqrt(x) for x in _to_host(list(var.unbind(0)))]
+            for j, layer in enumerate(layers):
+                key = str(layer)
+                if include_scores:
+                    means[key] = mean_list[j]
+                    stds[key] = std_list[j]
+                masks[key] = mask_list[j]
+                counts[key] = int(self.score_counts[layer])
+        else:
+            # sums on the host (accumulate_on_host): the reference's host math
+            pres = _to_host([self.score_presence_sums[i] for i in layers])
+            sums = _to_host([self.score_sums[i] for i in layers])
+            sq_sums = _to_host([self.score_sq_sums[i] for i in layers])
+            for j, layer in enumerate(layers):
+                key = str(layer)
+                presence = pres[j].clamp_min(1.0)
+                mean = sums[j] / presence
+                var = (sq_sums[j] / presence - mean.square()).clamp_min_(0.0)
+                means[key] = mean
+                stds[key] = torch.sqrt(var)
+                counts[key] = int(self.score_counts[layer])
+            for layer, m in zip(layers, _build_direct_mean_coverage_masks([means[str(i)] for i in layers], cfg)):
+                masks[str(layer)] = m.cpu()
         return {
             "version": 3,
             "config": asdict(cfg),
