@@ -331,7 +331,8 @@ class ZImageSinkMaskCalibrator:
         layers = sorted(self.score_sums)
         if not layers:
             pass
-        elif all(self.score_sums[i].is_cuda for i in layers):
+        elif all(self.score_sums[i].is_cuda and self.score_sums[i].shape == self.score_sums[layers[0]].shape
+                 and self.score_sums[i].device == self.score_sums[layers[0]].device for i in layers):
             # mean and std on the device, all layers at once (elementwise IEEE divisions by the
             # presence counts, as the reference's host math); the masks are built from the
             # device means and only what the package holds comes to the host
@@ -354,7 +355,7 @@ class ZImageSinkMaskCalibrator:
                 masks[key] = mask_list[j]
                 counts[key] = int(self.score_counts[layer])
         else:
-            # sums on the host (accumulate_on_host): the reference's host math
+            # sums on the host (accumulate_on_host, or mixed shapes): the reference's host math
             pres = _to_host([self.score_presence_sums[i] for i in layers])
             sums = _to_host([self.score_sums[i] for i in layers])
             sq_sums = _to_host([self.score_sq_sums[i] for i in layers])
