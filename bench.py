@@ -379,6 +379,9 @@ def main():
         scores = scores / scores.sum(-1, keepdim=True)
         mus = time_fn(torch, lambda: ops.coverage_mask(scores, 0.85, True), 10, 2) * 1e3
         out["coverage_mask_us"] = round(mus, 1)
+        # a mask the drop-in has not seen yet costs one plan (lists + launch order) first
+        plus = time_fn(torch, lambda: ops.block_sparse_plan(mask), 10, 3) * 1e3
+        out["plan_us"] = round(plus, 1)
         out["zimage_layer"] = zimage_layer(torch, dev, ops, sa, args)
         out["wan_calibration_pass"] = wan_calibration(torch, dev, sa)
         out["wan_attention_stack"] = wan_stack(torch, dev, ops, q, k, v)

@@ -46,10 +46,12 @@ int sinkattn_abi_version(void);
  * the external kernel consumed the bool mask directly; here it is turned once into
  *   counts[B*H*nqb]          number of listed key blocks per row,
  *   idx[B*H*nqb*nkb]         the listed key blocks of row r in idx[r*nkb .. r*nkb+counts[r]),
- *   order[slots]             launch order, slots = sinkattn_block_sparse_order_slots():
- *                            work-group i (on XCD i % 8) runs row order[i] (-1: none);
- *                            XCD x gets the q-blocks qb = x mod 8 of every (b, h), head
- *                            by head, longest first within a head.
+ *   order[n]                 n = sinkattn_block_sparse_order_slots() int32 entries: the
+ *                            launch slots (work-group i, on XCD i % 8, runs row order[i];
+ *                            -1: none), then a chunk table the plan uses internally.
+ *                            Each head's q-blocks go to the XCDs in chunks (longest-
+ *                            processing-time first over the XCDs, long rows leading each
+ *                            XCD's sequence), so an XCD's L2 holds few heads' K/V at once.
  * `mask` is uint8/bool [B,H,nqb,nkb] with element strides mask_strides[4].
  * ---------------------------------------------------------------------------------- */
 int64_t sinkattn_block_sparse_order_slots(int64_t B, int64_t H, int64_t nqb);

@@ -755,172 +755,246 @@ __host__ __device__ inline ChunkLayout chunk_layout(int nbh, int nqb) {
   return L;
 }
 
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanWaves = kPlanThreads / 64;
+
+// Chunked plans keep a chunk table after the launch slots of the order buffer, written by
+// plan_order_kernel and read by plan_chunk_sort_kernel: [0, 8) q-blocks per XCD, [8, 24)
+// cost sum per XCD (low, high word), [24] outliers taken out (1) or not (0), then per chunk
+// ch [32 + 2ch] its first slot along its XCD's sequence and [33 + 2ch] its XCD.
+constexpr int kMetaHead = 32;
+
+__host__ __device__ inline int chunk_size(const ChunkLayout& L, int nqb, int ch) {
+  const int C = ch < L.nw ? L.Cw : L.Cs;
+  const int j = ch < L.nw ? ch % L.Cw : (ch - L.nw) % L.Cs;
+  return (nqb - j + C - 1) / C;
+}
+
+// chunk ch -> (head, residue j, modulus)
+__device__ __forceinline__ void chunk_head(const ChunkLayout& L, int ch, int& bh, int& j, int& C) {
+  if (ch < L.nw) {
+    bh = ch / L.Cw;
+    j = ch - bh * L.Cw;
+    C = L.Cw;
+  } else {
+    const int f = ch - L.nw;
+    bh = L.nbh_w + f / L.Cs;
+    j = f % L.Cs;
+    C = L.Cs;
+  }
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 template <bool STAGED>
-__global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
+__global__ __launch_bounds__(kPlanThreads) void plan_order_kernel(PlanArgs a) {
   __shared__ int cost[kMaxChunks];
   __shared__ int16_t sorted[kMaxChunks + 2 * kXcds];  // later also 8 * (cap_s + cap_w)
+  __shared__ int scost[kMaxChunks];                   // cost of the r-th ranked chunk
   __shared__ uint8_t xcd[kMaxChunks];
   __shared__ int16_t pos[kMaxChunks];
-  // The passes below read each q-block's tile count many times.  STAGED (rows <=
+  // The passes below read each q-block's tile count several times.  STAGED (rows <=
   // kPlanLdsRows): they are copied to LDS once (eight coalesced loads in flight per
   // thread) and read there; otherwise they are read from global memory.
   __shared__ int cnt_lds[STAGED ? kPlanLdsRows : 1];
+  __shared__ unsigned long long xsum[kXcds];
+  __shared__ int xcnt[kXcds], nout[kXcds], nlist;
+  __shared__ int outl[kMaxOutliers], outl_c[kMaxOutliers];
+  __shared__ uint8_t outl_x[kMaxOutliers];
+  __shared__ int16_t nonout[kMaxChunks];
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63, wv = tid >> 6;
   const ChunkLayout L = chunk_layout(a.rows / a.nqb, a.nqb);
   const int nch = L.nw + L.ns;
   const int total = L.slots_per_xcd() * kXcds;
   if constexpr (STAGED) {
-    for (int base = 0; base < a.rows; base += 8 * 256) {
+    for (int base = 0; base < a.rows; base += 8 * kPlanThreads) {
       int v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int i = base + u * 256 + (int)threadIdx.x;
+        const int i = base + u * kPlanThreads + tid;
         v[u] = i < a.rows ? a.counts[i] : 0;
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int i = base + u * 256 + (int)threadIdx.x;
+        const int i = base + u * kPlanThreads + tid;
         if (i < a.rows) cnt_lds[i] = v[u];
       }
     }
-    __syncthreads();
   }
+  for (int i = tid; i < total; i += kPlanThreads) a.order[i] = -1;
+  if (tid < kXcds) {
+    xsum[tid] = 0;
+    xcnt[tid] = nout[tid] = 0;
+  }
+  if (tid == 0) nlist = 0;
+  __syncthreads();
   auto counts = [&](int row) __attribute__((always_inline)) {
     if constexpr (STAGED) return cnt_lds[row];
     else return a.counts[row];
   };
-  // chunk ch -> (head, residue j, modulus)
-  auto chunk_head = [&](int ch, int& bh, int& j, int& C) {
-    if (ch < L.nw) {
-      bh = ch / L.Cw;
-      j = ch - bh * L.Cw;
-      C = L.Cw;
-    } else {
-      const int f = ch - L.nw;
-      bh = L.nbh_w + f / L.Cs;
-      j = f % L.Cs;
-      C = L.Cs;
-    }
-  };
-  for (int i = threadIdx.x; i < total; i += blockDim.x) a.order[i] = -1;
-  for (int ch = threadIdx.x; ch < nch; ch += blockDim.x) {
+  // chunk costs: one wave per chunk, its lanes striding over the chunk's q-blocks
+  for (int ch = wv; ch < nch; ch += kPlanWaves) {
     int bh, j, C;
-    chunk_head(ch, bh, j, C);
+    chunk_head(L, ch, bh, j, C);
     int w = 0;
-    for (int qb = j; qb < a.nqb; qb += C) w += counts(bh * a.nqb + qb) + kQblockCost;
-    cost[ch] = w;
+    for (int qb = j + lane * C; qb < a.nqb; qb += 64 * C) w += counts(bh * a.nqb + qb) + kQblockCost;
+    w = wave_sum_i32(w);
+    if (lane == 0) cost[ch] = w;
   }
   __syncthreads();
   // rank by cost desc, index asc, within each kind (whole chunks, then fine chunks)
-  for (int ch = threadIdx.x; ch < nch; ch += blockDim.x) {
+  for (int ch = tid; ch < nch; ch += kPlanThreads) {
     const int lo = ch < L.nw ? 0 : L.nw, hi = ch < L.nw ? L.nw : nch;
     const int w = cost[ch];
     int r = lo;
     for (int c2 = lo; c2 < hi; ++c2) r += (cost[c2] > w) || (cost[c2] == w && c2 < ch);
     sorted[r] = (int16_t)ch;
+    scost[r] = w;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int load[kXcds], n[kXcds];
-    for (int x = 0; x < kXcds; ++x) load[x] = 0;
+  // Longest processing time first, one kind after the other: each chunk to the XCD with
+  // the least load (the lowest index among equals) that has room for one more of its kind.
+  // Wave 0 walks the ranking 64 chunks at a time (lane k holds the k-th chunk's cost).
+  // Lane x < 8 holds XCD x's load and count; the choice is the minimum over those lanes of
+  // load * 8 + x (three DPP steps), or, when the loads could pass 2^28, a scalar scan.
+  if (wv == 0) {
+    int64_t all = 0;
+    for (int r = lane; r < nch; r += 64) all += scost[r];
+    bool small = true;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) all += __shfl_xor(all, off, 64);
+    small = all < (1ll << 28);
+    int load = 0, nx = 0;  // lane x < 8: XCD x
     for (int kind = 0; kind < 2; ++kind) {
       const int lo = kind == 0 ? 0 : L.nw, hi = kind == 0 ? L.nw : nch;
       const int cap = kind == 0 ? L.cap_w : L.cap_s;
-      for (int x = 0; x < kXcds; ++x) n[x] = 0;
-      for (int r = lo; r < hi; ++r) {
-        const int ch = sorted[r];
-        int best = -1;
-        for (int x = 0; x < kXcds; ++x)
-          if (n[x] < cap && (best < 0 || load[x] < load[best])) best = x;
-        xcd[ch] = (uint8_t)best;
-        load[best] += cost[ch];
-        ++n[best];
+      nx = 0;
+      for (int rb = lo; rb < hi; rb += 64) {
+        const int rr = rb + lane;
+        const int wl = rr < hi ? scost[rr] : 0;
+        int mine = 0;
+        const int m = min(64, hi - rb);
+        for (int k = 0; k < m; ++k) {
+          const int w = __builtin_amdgcn_readlane(wl, k);
+          int best;
+          if (small) {
+            int key = (lane < kXcds && nx < cap) ? load * 8 + lane : 0x7fffffff;
+            key = min(key, __builtin_amdgcn_mov_dpp(key, 0xB1, 0xF, 0xF, false));   // lane ^ 1
+            key = min(key, __builtin_amdgcn_mov_dpp(key, 0x4E, 0xF, 0xF, false));   // lane ^ 2
+            key = min(key, __builtin_amdgcn_mov_dpp(key, 0x141, 0xF, 0xF, false));  // 7 - lane (within 8)
+            best = __builtin_amdgcn_readfirstlane(key) & 7;
+          } else {
+            best = -1;
+            int bl = 0;
+#pragma unroll
+            for (int x = 0; x < kXcds; ++x) {
+              const int lx = __builtin_amdgcn_readlane(load, x), nxx = __builtin_amdgcn_readlane(nx, x);
+              const bool take = nxx < cap && (best < 0 || lx < bl);
+              best = take ? x : best;
+              bl = take ? lx : bl;
+            }
+          }
+          load += lane == best ? w : 0;
+          nx += lane == best ? 1 : 0;
+          mine = lane == k ? best : mine;
+        }
+        if (rr < hi) xcd[sorted[rr]] = (uint8_t)mine;
       }
-      for (int x = 0; x < kXcds; ++x) n[x] = 0;
-      for (int ch = lo; ch < hi; ++ch) pos[ch] = (int16_t)(n[xcd[ch]]++);
     }
   }
   __syncthreads();
+  // each chunk's position among its XCD's chunks of the same kind (chunk order), and the
+  // XCD totals
+  for (int ch = tid; ch < nch; ch += kPlanThreads) {
+    const int lo = ch < L.nw ? 0 : L.nw;
+    const int x = xcd[ch];
+    int p = 0;
+    for (int c2 = lo; c2 < ch; ++c2) p += xcd[c2] == x;
+    pos[ch] = (int16_t)p;
+    atomicAdd(&xsum[x], (unsigned long long)cost[ch]);
+    atomicAdd(&xcnt[x], chunk_size(L, a.nqb, ch));
+  }
   // Sequence of each XCD: its outliers first (q-blocks costing more than twice the XCD's
   // mean, longest first: a long row started late ends the launch late), then its fine
   // chunks, then its whole chunks (each kind by position), each chunk's other q-blocks
   // longest first.  Outliers are fewer than half of an XCD's q-blocks; past kMaxOutliers
   // in the whole plan none are taken out (the chunk sequence alone).
-  __shared__ int xsum[kXcds], xcnt[kXcds], nout[kXcds], nlist;
-  __shared__ int outl[kMaxOutliers], outl_c[kMaxOutliers];
-  __shared__ uint8_t outl_x[kMaxOutliers];
-  __shared__ int wave_keys[4][256];
-  __shared__ int16_t nonout[kMaxChunks];
-  int* chunk_off = cost;   // the chunk costs are spent once the XCDs are assigned
-  int16_t* seq = sorted;   // so is the ranking: it becomes each XCD's chunk sequence
-  if (threadIdx.x < kXcds) xsum[threadIdx.x] = xcnt[threadIdx.x] = nout[threadIdx.x] = 0;
-  if (threadIdx.x == 0) nlist = 0;
-  // seq[x * (cap_s + cap_w) + k]: the k-th chunk of XCD x (fine chunks, then whole)
+  int16_t* seq = sorted;   // the ranking is spent: it becomes each XCD's chunk sequence
   const int per_x = L.cap_s + L.cap_w;
-  for (int i = threadIdx.x; i < per_x * kXcds; i += blockDim.x) seq[i] = -1;
   __syncthreads();
-  for (int ch = threadIdx.x; ch < nch; ch += blockDim.x)
+  for (int i = tid; i < per_x * kXcds; i += kPlanThreads) seq[i] = -1;
+  __syncthreads();
+  for (int ch = tid; ch < nch; ch += kPlanThreads)
     seq[xcd[ch] * per_x + (ch < L.nw ? L.cap_s : 0) + pos[ch]] = (int16_t)ch;
-  auto chunk_of = [&](int row, int& C, int& j) {
-    const int bh = row / a.nqb, qb = row - bh * a.nqb;
-    const bool fine = bh >= L.nbh_w;
-    C = fine ? L.Cs : L.Cw;
-    j = qb % C;
-    return fine ? L.nw + (bh - L.nbh_w) * L.Cs + j : bh * L.Cw + j;
-  };
-  for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
-    int C, j;
-    const int x = xcd[chunk_of(row, C, j)];
-    atomicAdd(&xsum[x], counts(row) + kQblockCost);
-    atomicAdd(&xcnt[x], 1);
-  }
-  __syncthreads();
-  // a q-block of `c` tiles on XCD x is an outlier when (c + kQblockCost) * count > 2 * sum
-  auto above = [&](int c, int x) __attribute__((always_inline)) {
-    return (int64_t)(c + kQblockCost) * xcnt[x] > 2 * (int64_t)xsum[x];
-  };
-  for (int row = threadIdx.x; row < a.rows; row += blockDim.x) {
-    int C, j;
-    const int x = xcd[chunk_of(row, C, j)];
-    if (above(counts(row), x)) {
-      atomicAdd(&nout[x], 1);
-      const int k = atomicAdd(&nlist, 1);
-      if (k < kMaxOutliers) outl[k] = row;
+  // outliers, one wave per chunk: a q-block of `c` tiles on XCD x is an outlier when
+  // (c + kQblockCost) * count > 2 * sum; nonout[ch] holds the chunk's outlier count for now
+  for (int ch = wv; ch < nch; ch += kPlanWaves) {
+    int bh, j, C;
+    chunk_head(L, ch, bh, j, C);
+    const int x = xcd[ch];
+    const int64_t xc = xcnt[x], xs2 = 2 * (int64_t)xsum[x];
+    int nch_out = 0;
+    for (int q0 = j; q0 < a.nqb; q0 += 64 * C) {
+      const int qb = q0 + lane * C;
+      const int row = bh * a.nqb + qb;
+      const bool is_out = qb < a.nqb && (int64_t)(counts(row) + kQblockCost) * xc > xs2;
+      const uint64_t mk = __ballot(is_out);
+      const int n_here = __popcll(mk);
+      if (n_here == 0) continue;
+      int base = 0;
+      if (lane == 0) base = atomicAdd(&nlist, n_here);
+      base = __shfl(base, 0, 64);
+      const int k = base + __popcll(mk & ((1ull << lane) - 1ull));
+      if (is_out && k < kMaxOutliers) outl[k] = row;
+      nch_out += n_here;
+    }
+    if (lane == 0) {
+      nonout[ch] = (int16_t)nch_out;
+      if (nch_out) atomicAdd(&nout[x], nch_out);
     }
   }
   __syncthreads();
   const bool use_out = nlist <= kMaxOutliers;
+  for (int ch = tid; ch < nch; ch += kPlanThreads) {  // non-outlier count per chunk
+    const int S = chunk_size(L, a.nqb, ch);
+    nonout[ch] = (int16_t)(use_out ? S - nonout[ch] : S);
+  }
   if (use_out) {  // XCD and tile count of every listed outlier
-    for (int k = threadIdx.x; k < nlist; k += blockDim.x) {
+    for (int k = tid; k < nlist; k += kPlanThreads) {
       const int r = outl[k];
-      int C, j;
-      outl_x[k] = xcd[chunk_of(r, C, j)];
+      const int bh = r / a.nqb, qb = r - bh * a.nqb;
+      const bool fine = bh >= L.nbh_w;
+      const int C = fine ? L.Cs : L.Cw;
+      const int ch = fine ? L.nw + (bh - L.nbh_w) * L.Cs + qb % C : bh * L.Cw + qb % C;
+      outl_x[k] = xcd[ch];
       outl_c[k] = counts(r);
     }
   }
-  for (int ch = threadIdx.x; ch < nch; ch += blockDim.x) {  // non-outlier count per chunk
-    int bh, j, C;
-    chunk_head(ch, bh, j, C);
-    const int64_t xc = xcnt[xcd[ch]], xs2 = 2 * (int64_t)xsum[xcd[ch]];
-    int n = 0;
-    for (int qb = j; qb < a.nqb; qb += C)
-      n += !(use_out && (int64_t)(counts(bh * a.nqb + qb) + kQblockCost) * xc > xs2);
-    nonout[ch] = (int16_t)n;
-  }
   __syncthreads();
-  if (threadIdx.x < kXcds) {  // offsets along each XCD's chunk sequence
-    const int x = threadIdx.x;
+  int32_t* meta = a.order + total;
+  if (tid < kXcds) {  // offsets along each XCD's chunk sequence
+    const int x = tid;
     int off = use_out ? nout[x] : 0;
     for (int k = 0; k < per_x; ++k) {
       const int ch = seq[x * per_x + k];
       if (ch < 0) continue;
-      chunk_off[ch] = off;
+      meta[kMetaHead + 2 * ch] = off;
       off += nonout[ch];
     }
+    meta[x] = xcnt[x];
+    meta[8 + 2 * x] = (int32_t)(xsum[x] & 0xffffffffull);
+    meta[9 + 2 * x] = (int32_t)(xsum[x] >> 32);
   }
-  __syncthreads();
+  if (tid == 0) meta[24] = use_out ? 1 : 0;
+  for (int ch = tid; ch < nch; ch += kPlanThreads) meta[kMetaHead + 2 * ch + 1] = xcd[ch];
   // Outliers: rank among the XCD's outliers by cost desc, then row asc.
   if (use_out) {
-    for (int k = threadIdx.x; k < nlist; k += blockDim.x) {
+    for (int k = tid; k < nlist; k += kPlanThreads) {
       const int r = outl[k], x = outl_x[k], c = outl_c[k];
       int slot = 0;
       for (int k2 = 0; k2 < nlist; ++k2) {
@@ -930,51 +1004,51 @@ __global__ __launch_bounds__(256) void plan_order_kernel(PlanArgs a) {
       a.order[slot * kXcds + x] = r;
     }
   }
-  // The other q-blocks: one wave per chunk.  A chunk has at most 255 q-blocks (chunks
-  // split heads of >= 128 q-blocks into pieces of 128-255), four per lane.  Their keys go
-  // to the wave's LDS row in q order: count * 256 + (255 - k) for the k-th q-block of the
-  // chunk (more tiles first, then lower q), -1 for an outlier and past the chunk's end.
-  // Every lane ranks its four against the row, 16 bytes per broadcast read, with one
-  // comparison per pair and no branches.
-  {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    int* keys = wave_keys[wv];
-    for (int ch = wv; ch < nch; ch += 4) {
-      int bh, j, C;
-      chunk_head(ch, bh, j, C);
-      const int S = (a.nqb - j + C - 1) / C;
-      const int x = xcd[ch];
-      const int64_t xc = use_out ? xcnt[x] : 0, xs2 = 2 * (int64_t)xsum[x];
-      int key[4];
+}
+
+// The other q-blocks of chunk blockIdx.x (one wave; the chunk table from plan_order_kernel).
+// A chunk has at most 255 q-blocks (chunks split heads of >= 128 q-blocks into pieces of
+// 128-255), four per lane.  Their keys go to LDS in q order: count * 256 + (255 - k) for
+// the k-th q-block of the chunk (more tiles first, then lower q), -1 for an outlier and
+// past the chunk's end.  Every lane ranks its four against the row, 16 bytes per broadcast
+// read, with one comparison per pair and no branches.
+__global__ __launch_bounds__(64) void plan_chunk_sort_kernel(PlanArgs a) {
+  __shared__ int keys[256];
+  const int lane = (int)threadIdx.x;
+  const int ch = (int)blockIdx.x;
+  const ChunkLayout L = chunk_layout(a.rows / a.nqb, a.nqb);
+  const int32_t* meta = a.order + L.slots_per_xcd() * kXcds;
+  int bh, j, C;
+  chunk_head(L, ch, bh, j, C);
+  const int S = (a.nqb - j + C - 1) / C;
+  const int off = meta[kMetaHead + 2 * ch], x = meta[kMetaHead + 2 * ch + 1];
+  const bool use_out = meta[24] != 0;
+  const int64_t xsum = (int64_t)(((uint64_t)(uint32_t)meta[9 + 2 * x] << 32) | (uint32_t)meta[8 + 2 * x]);
+  const int64_t xc = use_out ? meta[x] : 0, xs2 = 2 * xsum;
+  int key[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int k = lane + 64 * u;
-        key[u] = -1;
-        if (k < S) {
-          const int c = counts(bh * a.nqb + j + k * C);
-          if ((int64_t)(c + kQblockCost) * xc <= xs2) key[u] = c * 256 + (255 - k);
-        }
-        keys[k] = key[u];
-      }
-      // the wave's LDS writes land before its reads (in order within a wave)
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-      __builtin_amdgcn_wave_barrier();
-      int rank[4] = {0, 0, 0, 0};
-      for (int k2 = 0; k2 < S; k2 += 4) {
-        const i32x4 v = *reinterpret_cast<const i32x4*>(keys + k2);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int u = 0; u < 4; ++u) rank[u] += v[e] > key[u];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int k = lane + 64 * u;
-        if (key[u] >= 0) a.order[(chunk_off[ch] + rank[u]) * kXcds + x] = bh * a.nqb + j + k * C;
-      }
-      // every lane has read the row before the next chunk overwrites it
-      __builtin_amdgcn_wave_barrier();
+  for (int u = 0; u < 4; ++u) {
+    const int k = lane + 64 * u;
+    key[u] = -1;
+    if (k < S) {
+      const int c = a.counts[bh * a.nqb + j + k * C];
+      if ((int64_t)(c + kQblockCost) * xc <= xs2) key[u] = c * 256 + (255 - k);
     }
+    keys[k] = key[u];
+  }
+  __syncthreads();
+  int rank[4] = {0, 0, 0, 0};
+  for (int k2 = 0; k2 < S; k2 += 4) {
+    const i32x4 v = *reinterpret_cast<const i32x4*>(keys + k2);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) rank[u] += v[e] > key[u];
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int k = lane + 64 * u;
+    if (key[u] >= 0) a.order[(off + rank[u]) * kXcds + x] = bh * a.nqb + j + k * C;
   }
 }
 
@@ -1003,11 +1077,20 @@ static bool chunked_order(int rows, int nqb) {
   return L.nw + L.ns <= kMaxChunks;
 }
 
-int plan_order_slots(int rows, int nqb) {
+// Work-groups of a forward launch over a plan's order: its launch slots.
+static int plan_launch_slots(int rows, int nqb) {
   if (rows == 0 || nqb == 0) return 0;
   const int nbh = rows / nqb;
   if (!chunked_order(rows, nqb)) return nbh * ((nqb + kXcds - 1) / kXcds) * kXcds;
   return chunk_layout(nbh, nqb).slots_per_xcd() * kXcds;
+}
+
+// int32 entries of the order buffer: the launch slots, then (chunked plans) the chunk table.
+int plan_order_slots(int rows, int nqb) {
+  const int slots = plan_launch_slots(rows, nqb);
+  if (slots == 0 || !chunked_order(rows, nqb)) return slots;
+  const ChunkLayout L = chunk_layout(rows / nqb, nqb);
+  return slots + kMetaHead + 2 * (L.nw + L.ns);
 }
 
 hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream) {
@@ -1015,18 +1098,23 @@ hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream) {
   plan_rows_kernel<<<(a.rows + 3) / 4, 256, 0, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.order == nullptr) return e;
-  if (chunked_order(a.rows, a.nqb) && a.rows <= kPlanLdsRows)
-    plan_order_kernel<true><<<1, 256, 0, stream>>>(a);
-  else if (chunked_order(a.rows, a.nqb))
-    plan_order_kernel<false><<<1, 256, 0, stream>>>(a);
-  else
+  if (chunked_order(a.rows, a.nqb)) {
+    if (a.rows <= kPlanLdsRows)
+      plan_order_kernel<true><<<1, kPlanThreads, 0, stream>>>(a);
+    else
+      plan_order_kernel<false><<<1, kPlanThreads, 0, stream>>>(a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const ChunkLayout L = chunk_layout(a.rows / a.nqb, a.nqb);
+    plan_chunk_sort_kernel<<<L.nw + L.ns, 64, 0, stream>>>(a);
+  } else
     plan_order_interleaved_kernel<<<1, 256, 0, stream>>>(a);
   return hipGetLastError();
 }
 
 static int fwd_grid(const FwdArgs& a) {
   const int rows = a.B * a.H * a.nqb;
-  return a.order ? plan_order_slots(rows, a.nqb) : rows;
+  return a.order ? plan_launch_slots(rows, a.nqb) : rows;
 }
 
 template <int IT, int CT>

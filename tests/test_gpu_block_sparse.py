@@ -221,11 +221,13 @@ def _check_order(plan, counts, nbh, nqb):
     chunk's cost."""
     L = _chunk_layout(nbh, nqb)
     cap_w, cap_s = -(-L["nw"] // 8), -(-L["ns"] // 8)
-    order = plan.order.cpu().tolist()
+    slots = (cap_w * L["Sw"] + cap_s * L["Ss"]) * 8
+    # the launch slots, then the plan's chunk table (32 + 2 ints per chunk)
+    assert plan.order.numel() == slots + 32 + 2 * (L["nw"] + L["ns"])
+    order = plan.order.cpu().tolist()[:slots]
     rows = nbh * nqb
     real = sorted(r for r in order if r >= 0)
     assert real == list(range(rows))
-    assert len(order) == (cap_w * L["Sw"] + cap_s * L["Ss"]) * 8
 
     def chunk_of(r):
         bh, qb = divmod(r, nqb)
