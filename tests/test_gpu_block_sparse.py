@@ -302,6 +302,38 @@ def test_plan_order_long_rows_first(B, H, nqb, full, density):
     _check_order(plan, plan.counts.cpu(), B * H, nqb)
 
 
+def test_plan_order_many_heads_interleaved():
+    # More than 4096 chunks (here 4100 heads of 20 q-blocks): the plan falls back to the
+    # interleaved order.  Slot (bh * S + k) * 8 + x (S = ceil(nqb / 8)) holds the k-th
+    # q-block of head bh with qb = x mod 8, by tile count desc then qb asc, -1 past the end;
+    # the forward over that order matches the oracle on sampled heads.
+    B, H, nqb, D = 1, 4100, 20, 128
+    N = nqb * 128
+    g = torch.Generator(device="cuda").manual_seed(60)
+    q, k, v = (torch.randn(B, H, N, D, device="cuda", dtype=torch.bfloat16, generator=g) for _ in range(3))
+    mask = _random_mask(B, H, nqb, nqb, 0.3, seed=61)
+    plan = ops.block_sparse_plan(mask)
+    S = -(-nqb // 8)
+    assert plan.order.numel() == B * H * S * 8
+    order = plan.order.cpu().view(B * H, S, 8)
+    counts = plan.counts.cpu().view(B * H, nqb)
+    want = torch.full((B * H, S, 8), -1, dtype=torch.int32)
+    for x in range(8):
+        qbs = torch.arange(x, nqb, 8)
+        c = counts[:, qbs]  # [heads, n]
+        # by count desc, then qb asc: sort on count * nqb + (nqb - 1 - qb), descending
+        key = c * nqb + (nqb - 1 - qbs).unsqueeze(0)
+        rank = torch.argsort(key, dim=1, descending=True)
+        rows = torch.arange(B * H).unsqueeze(1) * nqb + qbs[rank]
+        want[:, : qbs.numel(), x] = rows.to(torch.int32)
+    assert torch.equal(order, want)
+    out, lse = ops.block_sparse_attention(q, k, v, plan)
+    torch.cuda.synchronize()
+    heads = torch.tensor([0, 1, 2047, 4096, 4099])
+    sub = lambda t: t[:, heads.cuda()]  # noqa: E731
+    _check(sub(out), sub(lse), sub(q), sub(k), sub(v), sub(mask))
+
+
 def test_bad_mask_shape_raises():
     q, k, v = _inputs(1, 2, 256, 256, 128, torch.bfloat16, seed=1)
     with pytest.raises(ValueError):
