@@ -865,10 +865,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_order_kernel(PlanArgs a) {
   if (wv == 0) {
     int64_t all = 0;
     for (int r = lane; r < nch; r += 64) all += scost[r];
-    bool small = true;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) all += __shfl_xor(all, off, 64);
-    small = all < (1ll << 28);
+    const bool small = all < (1ll << 28);  // every load * 8 + 7 fits an int
     int load = 0, nx = 0;  // lane x < 8: XCD x
     for (int kind = 0; kind < 2; ++kind) {
       const int lo = kind == 0 ? 0 : L.nw, hi = kind == 0 ? L.nw : nch;

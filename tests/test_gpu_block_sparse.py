@@ -302,6 +302,19 @@ def test_plan_order_long_rows_first(B, H, nqb, full, density):
     _check_order(plan, plan.counts.cpu(), B * H, nqb)
 
 
+def test_plan_order_large_costs():
+    # 32768 dense q-blocks of 8192 key blocks: the chunk costs add up past 2^28, where the
+    # launch-order pass picks each chunk's XCD by a scalar scan instead of the packed
+    # (load * 8 + XCD) minimum; the order keeps every invariant.
+    mask = torch.ones(1, 128, 256, 8192, dtype=torch.bool, device="cuda")
+    plan = ops.block_sparse_plan(mask)
+    counts = plan.counts.cpu()
+    assert int(counts.sum()) + 2 * counts.numel() >= 1 << 28
+    assert bool((counts == 8192).all())
+    del mask
+    _check_order(plan, counts, 128, 256)
+
+
 def test_plan_order_many_heads_interleaved():
     # More than 4096 chunks (here 4100 heads of 20 q-blocks): the plan falls back to the
     # interleaved order.  Slot (bh * S + k) * 8 + x (S = ceil(nqb / 8)) holds the k-th
