@@ -35,7 +35,8 @@ enum sinkattn_dtype { SINKATTN_BF16 = 0, SINKATTN_F16 = 1, SINKATTN_F32 = 2 };
 /* Message for the last non-zero status returned on the calling thread ("" if none). */
 const char* sinkattn_last_error(void);
 
-/* ABI version of this library (bumped on any signature change). */
+/* ABI version of this library (bumped on any change of a signature or of a buffer's
+ * contract; 3: the order buffer of a plan also holds its chunk table). */
 int sinkattn_abi_version(void);
 
 /* ------------------------------------------------------------------------------------

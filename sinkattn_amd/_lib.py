@@ -105,7 +105,7 @@ class SinkAttnError(RuntimeError):
 
 # Version of the entry-point signatures declared in include/sinkattn.h (raised whenever an
 # existing signature changes).
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 def load_library() -> ctypes.CDLL:

@@ -71,7 +71,7 @@ extern "C" {
 
 const char* sinkattn_last_error(void) { return g_last_error.c_str(); }
 
-int sinkattn_abi_version(void) { return 2; }
+int sinkattn_abi_version(void) { return 3; }
 
 int64_t sinkattn_block_sparse_order_slots(int64_t B, int64_t H, int64_t nqb) {
   if (B <= 0 || H <= 0 || nqb <= 0 || B * H * nqb > kMaxInt) return 0;
