@@ -174,6 +174,43 @@ def cpu_baseline(torch, q, k, v, mask, n_qblocks, total_flops_layer):
     }
 
 
+def config1_chain(torch, dev, sa, with_cpu):
+    """BASELINE config 1, the reference's CPU-runnable case, as the whole chain: fp32
+    [1,12,4096,128] N(0,1) with keys 0..3 x8 -> exact block mass -> coverage-0.85 mask ->
+    sparse attention on that mask.  GPU times of each drop-in step (inputs resident), and
+    with_cpu the same steps by the oracle (the reference's torch algorithms) on the host."""
+    B, H, N, D = 1, 12, 4096, 128
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(B, H, N, D, generator=g) for _ in range(3))
+    k[:, :, :4] *= 8.0
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    cfg = sa.SinkSparseConfig(pooling_mode="exact", offline_direct_coverage=0.85)
+    mass = sa._compute_block_scores(qd, kd, vd, cfg)
+    mean = mass.mean(dim=0)
+    mask = sa._build_direct_mean_coverage_mask(mean, cfg)
+    bmask = mask.unsqueeze(0)
+    pool_ms = time_fn(torch, lambda: sa._compute_block_scores(qd, kd, vd, cfg), 10, 3)
+    mask_ms = time_fn(torch, lambda: sa._build_direct_mean_coverage_mask(mean, cfg), 10, 3)
+    attn_ms = time_fn(torch, lambda: sa._block_sparse_attn(qd, kd, vd, bmask), 10, 3)
+    flops = tile_flops(torch, bmask, N, N, D)
+    out = {"shape": [B, H, N, D], "dtype": "f32", "mask_density": round(float(mask.float().mean()), 4),
+           "gpu_ms": {"pooling": round(pool_ms, 4), "mask": round(mask_ms, 4), "attention": round(attn_ms, 4)},
+           "attention_tflops": round(flops / (attn_ms * 1e-3) / 1e12, 2)}
+    if with_cpu:
+        from oracle import torch_ref  # the checker package, timed here as the CPU baseline
+        t0 = time.perf_counter()
+        cmass = torch_ref.exact_block_mass(q, k)
+        t1 = time.perf_counter()
+        cmask = torch_ref.coverage_mask(cmass.mean(dim=0), coverage=0.85, keep_diagonal=True)
+        t2 = time.perf_counter()
+        att = cpu_baseline(torch, q, k, v, cmask.unsqueeze(0), 0, flops)
+        out["cpu_ms"] = {"pooling": round((t1 - t0) * 1e3, 1), "mask": round((t2 - t1) * 1e3, 1),
+                         "attention": att["ms_per_layer"]}
+        out["cpu_threads"] = torch.get_num_threads()
+        out["cpu_mask_equal"] = bool(torch.equal(cmask, mask.cpu()))
+    return out
+
+
 def cpu_calibration_baseline(torch, ops, q, k, gpu_pool_ms, gpu_mask_us):
     """The calibration steps on the host, as the reference computes them (the oracle restates
     its torch ops): the exact block mass of one (b, h) pair of the config-2 layer, scaled to
@@ -385,6 +422,7 @@ def main():
         out["zimage_layer"] = zimage_layer(torch, dev, ops, sa, args)
         out["wan_calibration_pass"] = wan_calibration(torch, dev, sa)
         out["wan_attention_stack"] = wan_stack(torch, dev, ops, q, k, v)
+        out["config1_chain"] = config1_chain(torch, dev, sa, not args.no_cpu_baseline)
 
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, q, k, v, mask, args.cpu_sample_qblocks, flops)
