@@ -283,8 +283,10 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
     for (int i = 0; i < DT; ++i) o[i] *= alpha;
     m_run = m_tile;
   }
-  // P in the MFMA's 16-bit type; the row sum adds those rounded values (one dot2 per
-  // pair, four independent partial sums), so O and l are normalised by the same weights.
+  // P in the MFMA's 16-bit type for PV; the row sum adds the fp32 values before that
+  // rounding (four independent partial sums), as the flash-attention forward does.  Plain
+  // fp32 adds, not v_dot2 of the packed pairs: the dot2 instructions stall while the other
+  // wave's MFMAs run on the SIMD (~11 cycles each, measured), plain VALU does not.
   u32x4 p[4][2];
   float lsum[4] = {0.f, 0.f, 0.f, 0.f};
   auto make_p = [&](int t, int u) {
@@ -293,7 +295,7 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
       const float v0 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e], c, bias - m_run));
       const float v1 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e + 1], c, bias - m_run));
       p[t][u][e] = pack2<CT>(v0, v1);
-      lsum[t] = sum2_acc<CT>(p[t][u][e], lsum[t]);
+      lsum[t] += v0 + v1;
     }
   };
   // V^T operand for d-tile dt of step (t, u): two transpose reads.

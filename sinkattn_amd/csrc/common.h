@@ -41,21 +41,6 @@ __device__ __forceinline__ uint32_t pack2<kF16>(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
 }
 
-// acc + lo + hi of a packed pair of 16-bit floats, in one v_dot2c_f32_{bf16,f16} against
-// the constant pair (1, 1): the products are exact, the sum is fp32.
-template <int CT>
-__device__ __forceinline__ float sum2_acc(uint32_t packed, float acc);
-template <>
-__device__ __forceinline__ float sum2_acc<kBF16>(uint32_t packed, float acc) {
-  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed), one, acc, false);
-}
-template <>
-__device__ __forceinline__ float sum2_acc<kF16>(uint32_t packed, float acc) {
-  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), one, acc, false);
-}
-
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
