@@ -37,7 +37,7 @@ HBM_PEAK_GBS = 8000.0
 # 0.5 GiB for it -> x2.0, WRITE_SIZE reads 1 GiB -> x1.0).  Summaries with the commands:
 # profiles/block_sparse_fwd_wan_c2.md and profiles/block_mass_pool_wan_c2.md.
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
-TRAFFIC_KIB = {"fa": (1439910.0, 199631.0), "pool": (1278002.0, 792576.0)}
+TRAFFIC_KIB = {"fa": (1449431.0, 199631.0), "pool": (1278539.0, 792577.0)}
 
 
 def traffic_bytes(kind):
