@@ -1,8 +1,10 @@
 """GPU parity of the block-sparse attention forward (sinkattn_block_sparse_fwd) against
 the fp32 dense masked-softmax oracle (oracle/torch_ref.dense_masked_attention).
 
-Tolerance (north star): max |out - ref| <= 2e-2 and mean |out - ref| <= 1e-3; lse is
-compared in fp32 to 2e-2 absolute.
+Tolerance (north star): max |out - ref| <= 2e-2 and mean |out - ref| <= 1e-3.  The lse
+the kernels write (fp32, the row sums taken in fp32 as the flash-attention forward does) is
+held to 1e-3 + 1e-5 |ref|; the drop-in's lse, cast to q.dtype like the reference's, to 2e-2
+plus that type's rounding.
 """
 import math
 
@@ -58,9 +60,13 @@ def _check(out, lse, q, k, v, mask, rows=None, scale=None):
     assert err.mean().item() <= MEAN_ABS, err.mean().item()
     fin = torch.isfinite(ref_l)
     assert torch.equal(fin, torch.isfinite(l))
-    # lse from the drop-in API is cast to q.dtype like the reference's; allow that rounding
-    rnd = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}.get(lse.dtype, 0.0)
-    assert ((l[fin] - ref_l[fin]).abs() <= 2e-2 + rnd * ref_l[fin].abs()).all()
+    if lse.dtype == torch.float32:
+        assert ((l[fin] - ref_l[fin]).abs() <= 1e-3 + 1e-5 * ref_l[fin].abs()).all(), \
+            (l[fin] - ref_l[fin]).abs().max().item()
+    else:
+        # lse from the drop-in API is cast to q.dtype like the reference's; allow that rounding
+        rnd = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}[lse.dtype]
+        assert ((l[fin] - ref_l[fin]).abs() <= 2e-2 + rnd * ref_l[fin].abs()).all()
     assert torch.equal(o[~fin.unsqueeze(-1).expand_as(o)], torch.zeros_like(o[~fin.unsqueeze(-1).expand_as(o)]))
 
 
