@@ -6,8 +6,9 @@ math and on bf16 GPU tensors for the reference's exact op sequence), and
 `torch_ref.dense_masked_attention` for both attention branches.  Tolerances: pooling
 within one rounding of the dtype; the mix bit-exact with the reference's op sequence
 for bf16/f16 (one-ulp differences allowed on at most 1e-4 of the elements, for `exp`
-implementations that differ in the last fp32 bit), within 1e-5 relative for fp32; the fused attention 2e-2 max-abs / 1e-3 mean-abs
-against the fp32 union attention; against the reference's unfused sequence (whose LSEs
+implementations that differ in the last fp32 bit), within 1e-5 relative for fp32; the fused
+attention 2e-2 max-abs / 1e-3 mean-abs against the fp32 union attention, its fp32 lse within
+1e-3 + 1e-5|lse|; against the reference's unfused sequence (whose LSEs
 are rounded to bf16 before the mix) 2e-3 mean-abs and, per element, 2e-2 plus the
 largest shift that the reference's bf16 roundings of the LSEs and mix steps can cause."""
 import math
@@ -155,7 +156,8 @@ def test_fused_compensation_vs_oracle(N, gap, prefix, comp_rows, seed):
     # the kernel's row sums add the bf16-rounded P values it multiplies V with (relative
     # error <= 2^-9 per value), so the LSE is within 2^-8 of the fp32 one
     lerr = (lse.cpu() - want_lse).abs()
-    assert lerr.max().item() <= 2.0 ** -8 and lerr.mean().item() <= 5e-4
+    # fp32 lse with fp32 row sums: well inside 1e-3 (max 3e-6 at config 2 without compensation)
+    assert (lerr <= 1e-3 + 1e-5 * want_lse.abs()).all(), lerr.max().item()
     # against the reference's unfused sequence (bf16 LSEs into the reference-rounded mix)
     so, sl = sa._block_sparse_attn(q, k, v, m.to(DEV), return_lse=True)
     full = torch.ones(B, H, -(-cr // 128), -(-kd.size(2) // 128), dtype=torch.bool, device=DEV)
