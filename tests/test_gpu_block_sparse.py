@@ -96,6 +96,23 @@ def test_head_dims_32_and_64(dtype, D):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("Nq,Nk", [(1, 1), (1, 300), (130, 1), (700, 900), (900, 129)])
+def test_d128_tiny_and_unequal_lengths(dtype, Nq, Nk):
+    # the DMA-staged D=128 kernel on single rows / single keys, ragged last blocks on both
+    # sides and Nq != Nk; with one key the output is that key's v row and lse its logit
+    q, k, v = _inputs(1, 2, Nq, Nk, 128, dtype, seed=Nq * 1000 + Nk, sink_keys=1)
+    nqb, nkb = math.ceil(Nq / 128), math.ceil(Nk / 128)
+    mask = _random_mask(1, 2, nqb, nkb, 0.5, seed=Nk)
+    out, lse = ops.block_sparse_attention(q, k, v, ops.block_sparse_plan(mask))
+    torch.cuda.synchronize()
+    _check(out, lse, q, k, v, mask)
+    if Nk == 1:
+        assert torch.equal(out.float().cpu(), v.float().cpu().expand(-1, -1, Nq, -1))
+        logit = (q.float() @ k.float().transpose(-1, -2)).squeeze(-1).cpu() / math.sqrt(128)
+        assert (lse.cpu() - logit).abs().max().item() <= 1e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("step", [7.5, 30.0, -12.0])
 def test_running_maximum_moves_across_tiles(dtype, step):
     # Key block j gets a score offset of j * step log2 units (through channel 0: q = 1,
