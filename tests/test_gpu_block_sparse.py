@@ -377,12 +377,13 @@ def test_bad_mask_shape_raises():
 
 
 @pytest.mark.slow
-def test_wan_config2_full_size_rows_subsampled():
-    # BASELINE config 2 at full size: B=2, H=12, N=32760 (last block 120), bf16, sinks at
-    # frame-0 positions, 20% seeded mask + diagonal + column 0.  The oracle evaluates 48
-    # rows per (b, h) spread over the sequence, including the ragged last block.
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_wan_config2_full_size_rows_subsampled(dtype):
+    # BASELINE config 2 at full size: B=2, H=12, N=32760 (last block 120), bf16 (and f16),
+    # sinks at frame-0 positions, 20% seeded mask + diagonal + column 0.  The oracle
+    # evaluates 48 rows per (b, h) spread over the sequence, including the ragged last block.
     B, H, N = 2, 12, 32760
-    q, k, v = _inputs(B, H, N, N, 128, torch.bfloat16, seed=20)
+    q, k, v = _inputs(B, H, N, N, 128, dtype, seed=20)
     g = torch.Generator().manual_seed(21)
     sinks = torch.randint(0, 1560, (8,), generator=g)
     k[:, :, sinks.cuda()] *= 6.0
@@ -391,6 +392,10 @@ def test_wan_config2_full_size_rows_subsampled():
     torch.cuda.synchronize()
     rows = torch.cat([torch.randperm(N - 120, generator=g)[:40], torch.arange(N - 8, N)]).sort().values
     _check(out, lse[..., 0], q, k, v, mask, rows=rows)
+    # the kernel's own fp32 lse (the drop-in rounds it to q.dtype)
+    _, lse32 = ops.block_sparse_attention(q, k, v, ops.PLAN_CACHE.get(mask))
+    torch.cuda.synchronize()
+    _check(out, lse32, q, k, v, mask, rows=rows)
 
 
 @pytest.mark.slow
