@@ -8,7 +8,11 @@
  *    >0            a hipError_t from a launch
  * No C++ exception crosses this boundary and no entry point allocates device memory:
  * outputs and workspaces are supplied by the caller (sizes from the *_bytes queries).
- * Functions are stateless and reentrant; all work is stream-ordered.
+ * All work is stream-ordered.  Every function is stateless and reentrant except
+ * sinkattn_block_sparse_attn_noalloc (end of this file): it keeps its plan in one static
+ * device array per GPU (SINKATTN_NOALLOC_SCRATCH_BYTES = 32 MiB, reserved on every GPU
+ * that loads this library, whether or not that entry point is called), so calls of it that
+ * overlap on one GPU race.
  *
  * Tensor conventions.  A "BHSD" operand is addressed as
  *     base[b*s[0] + h*s[1] + n*s[2] + d*s[3]]   with s[3] == 1,
@@ -277,7 +281,11 @@ int sinkattn_coverage_mask(const float* scores, int64_t H, int64_t nq, int64_t n
  * needs 1.6 million).  Larger calls return an invalid-argument status.
  * The array keeps the last call's plan and is shared by all calls on one GPU: calls on one
  * stream are ordered, but calls that overlap on one GPU (several streams or threads at
- * once) race and must not be issued.
+ * once) race and must not be issued.  The array is part of the library's code object, so
+ * every GPU that loads the library reserves its 32 MiB, whether or not this function is
+ * called.  The first call on each GPU looks up the array's device address and must not run
+ * under stream capture (it returns an invalid-argument status there): make one call outside
+ * capture first; later calls may be captured into a graph.
  * ---------------------------------------------------------------------------------- */
 #define SINKATTN_NOALLOC_SCRATCH_BYTES (32u << 20)
 int sinkattn_block_sparse_attn_noalloc(const uint8_t* mask, const int64_t mask_strides[4],

@@ -32,14 +32,26 @@ int64_t align256(int64_t bytes) { return (bytes + 255) / 256 * 256; }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Device address of the current GPU's copy of `scratch` (looked up on first use per GPU).
-hipError_t scratch_on_current_device(void** out) {
+// Device address of the current GPU's copy of `scratch`, looked up on the first call per
+// GPU.  That lookup may load the library's code object on the GPU, which must not happen
+// while `stream` is being captured into a graph: an uncached first call under capture is
+// refused (*refused = true, nothing looked up), so callers make one call outside capture
+// first.
+hipError_t scratch_on_current_device(hipStream_t stream, void** out, bool* refused) {
+  *refused = false;
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_lookup_mutex);
   if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return e;
+    if (cs != hipStreamCaptureStatusNone) {
+      *refused = true;
+      return hipSuccess;
+    }
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return e;
@@ -77,8 +89,13 @@ extern "C" int sinkattn_block_sparse_attn_noalloc(
                         "plan buffer; use sinkattn_block_sparse_plan + sinkattn_block_sparse_fwd",
                         (long long)(counts_bytes + order_bytes + idx_bytes), (long long)cap);
   void* base = nullptr;
-  const int st = sa::api_hip_status(scratch_on_current_device(&base), "attn_noalloc: plan buffer address");
+  bool refused = false;
+  const int st = sa::api_hip_status(scratch_on_current_device(static_cast<hipStream_t>(stream), &base, &refused),
+                                    "attn_noalloc: plan buffer address");
   if (st != 0) return st;
+  if (refused)
+    return sa::api_fail("attn_noalloc: the first call on a GPU looks up the static plan buffer's address and "
+                        "must not run under stream capture; make one call outside capture first");
   unsigned char* p = static_cast<unsigned char*>(base);
   int32_t* counts = reinterpret_cast<int32_t*>(p);
   int32_t* order = reinterpret_cast<int32_t*>(p + counts_bytes);

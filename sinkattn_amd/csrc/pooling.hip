@@ -2,15 +2,22 @@
 //
 // block_mass_pool: the reference's exact mode, `_compute_exact_block_mass_scores`
 //   (sinkattention/sparse_attention.py:145-227), in one pass over K with no N x N
-//   intermediate.  A work-group owns one q-block (32*NW rows).  For every key tile it
-//   computes S^T with the matrix cores, turns each row's scores into exp2 terms relative
-//   to a per-row reference maximum, and keeps the per-(row, key-block) sums in LDS.  The
-//   reference maximum is only moved when a tile's maximum exceeds it by more than
-//   kRescaleMargin (log2 units); then the row's earlier sums are rescaled.  At the end
-//   every row is normalised by its own total and the rows are averaged per key block.
+//   intermediate.  A work-group owns one q-block (128 rows) at a time.  For every key tile
+//   it computes S^T with the matrix cores and turns each row's scores into exp2 terms
+//   relative to a per-row reference maximum.
+//   * bf16/f16 (block_mass_persistent_kernel): persistent groups; the per-(row, key-block)
+//     sums go to the group's slot ws[kb][row] of a global workspace.  The reference maximum
+//     is the row maximum of the first tile and moves only when a tile's sum exceeds 2^64
+//     (kSumLimit); then the row's earlier sums are rescaled.
+//   * fp32 (block_mass_f32_kernel): one group per q-block; the sums stay in LDS, and the
+//     reference maximum moves when a tile's maximum exceeds it by more than
+//     kRescaleMargin (log2 units), rescaling the earlier sums.
+//   At the end every row is normalised by its own total and the rows are averaged per key
+//   block.
 //
 // max_pool: `attn_with_pooling` (sinkattention/pooling_kernel.py:11-248) without the
-//   [B,H,N,nd] scratch: the per-(row, key-block) maxima live in LDS.
+//   [B,H,N,nd] scratch: the per-(row, key-block) maxima of the rows in flight go to the
+//   group's slot ws[kb][row] of a global workspace (max_pool_persistent_kernel).
 //
 // mean_pool: `_compute_pooled_qk_block_scores`' mean branch
 //   (sinkattention/sparse_attention.py:79-94,138-142).
@@ -21,7 +28,7 @@
 
 namespace sa {
 
-constexpr float kRescaleMargin = 8.f;
+constexpr float kRescaleMargin = 8.f;  // block_mass_f32_kernel only
 
 // ------------------------------------------------------------------------------------
 // Exact block mass, 16-bit inputs, persistent work-groups (up to 3 per CU).

@@ -258,6 +258,46 @@ def _build_direct_mean_coverage_masks(means: Sequence[torch.Tensor],
     return list(masks.to(home).unbind(0))
 
 
+def _device_package_groups(sums: Sequence[torch.Tensor], sq_sums: Sequence[torch.Tensor],
+                           denoms: Sequence[torch.Tensor], config: SinkSparseConfig, need_scores: bool,
+                           denom_min: Optional[float] = None, group_bytes: int = 256 << 20):
+    """The package's statistics of calibration sums that live on one GPU, layer by layer as
+    the reference's host math computes them: mean = sum / denom, var = clamp(sq / denom -
+    mean^2, 0) (elementwise IEEE operations, bit-identical on either side), and the coverage
+    masks of the means.  denoms[j] is a device tensor broadcastable to sums[j] (a layer's
+    call count, or Z-Image's presence counts, clamped below at `denom_min` when given).
+    Layers go in groups whose stacked sums take at most `group_bytes`, with in-place
+    arithmetic, so the transient device memory is about three such stacks (768 MB by
+    default) whatever the layer count.  Returns host lists: masks, and means and stds (None
+    unless need_scores; the square roots are taken on the host, since torch's device sqrt is
+    not correctly rounded)."""
+    per = max(1, sums[0].numel() * sums[0].element_size())
+    G = max(1, group_bytes // per)
+    args = _coverage_mask_args(sums[0], config)
+    masks: List[torch.Tensor] = []
+    means: Optional[List[torch.Tensor]] = [] if need_scores else None
+    stds: Optional[List[torch.Tensor]] = [] if need_scores else None
+    for g0 in range(0, len(sums), G):
+        sl = slice(g0, g0 + G)
+        den = torch.stack(list(denoms[sl]))
+        if denom_min is not None:
+            den.clamp_min_(denom_min)
+        mean = torch.stack(list(sums[sl]))
+        mean.div_(den)
+        masks.extend(_to_host([ops.coverage_mask(mean[i], *args) for i in range(mean.size(0))]))
+        if need_scores:
+            var = torch.stack(list(sq_sums[sl]))
+            var.div_(den)
+            sq = torch.mul(mean, mean)
+            var.sub_(sq)
+            del sq
+            var.clamp_min_(0.0)
+            means.extend(_to_host(list(mean.unbind(0))))
+            stds.extend(torch.sqrt(x) for x in _to_host(list(var.unbind(0))))
+        del mean, den
+    return masks, means, stds
+
+
 def _to_host(tensors: Sequence[torch.Tensor], chunk_bytes: int = 256 << 20) -> List[torch.Tensor]:
     """Host copies of equal-shaped tensors, stacked on their device in chunks of at most
     `chunk_bytes` so that one copy moves many of them (the values are untouched)."""
@@ -454,23 +494,14 @@ class SinkMaskCalibrator:
         on_device = first.is_cuda and all(self.score_sums[i].shape == first.shape
                                           and self.score_sums[i].device == first.device for i in layers)
         if on_device:
-            # Mean and std where the sums are, all layers at once.  The count is a device
+            # Mean and std where the sums are, in groups of layers.  The count is a device
             # tensor, so the division is an elementwise IEEE division, as the reference's host
             # division (a division by a Python number would be a multiply by its reciprocal).
-            sums = torch.stack([self.score_sums[i] for i in layers])
-            n = torch.tensor([float(self.score_counts[i]) for i in layers], device=first.device)
-            n = n.view(-1, *([1] * first.dim()))
-            mean = sums / n
-            del sums
-            masks = _build_direct_mean_coverage_masks(list(mean.unbind(0)), config)
-            # the package lives on the host: the masks always, the scores when asked for
-            masks = _to_host(masks)
-            means = stds = None
-            if need_scores:
-                var = (torch.stack([self.score_sq_sums[i] for i in layers]) / n - mean.square()).clamp_min_(0.0)
-                means = _to_host(list(mean.unbind(0)))
-                # the square root on the host: torch's device sqrt is not correctly rounded
-                stds = [torch.sqrt(x) for x in _to_host(list(var.unbind(0)))]
+            # The package lives on the host: the masks always, the scores when asked for.
+            n = [torch.full([1] * first.dim(), float(self.score_counts[i]), device=first.device) for i in layers]
+            masks, means, stds = _device_package_groups([self.score_sums[i] for i in layers],
+                                                        [self.score_sq_sums[i] for i in layers], n, config,
+                                                        need_scores)
         else:
             # sums on the host (accumulate_on_host, or mixed shapes): the reference's host math
             sums = _to_host([self.score_sums[i] for i in layers])

@@ -29,6 +29,7 @@ from .sparse_attention import (
     _block_sparse_attn_with_compensation,
     _build_direct_mean_coverage_mask,
     _build_direct_mean_coverage_masks,
+    _device_package_groups,
     _ceil_div,
     _compute_block_scores,
     _dense_short_attention_with_lse,
@@ -333,20 +334,12 @@ class ZImageSinkMaskCalibrator:
             pass
         elif all(self.score_sums[i].is_cuda and self.score_sums[i].shape == self.score_sums[layers[0]].shape
                  and self.score_sums[i].device == self.score_sums[layers[0]].device for i in layers):
-            # mean and std on the device, all layers at once (elementwise IEEE divisions by the
+            # mean and std on the device in groups of layers (elementwise IEEE divisions by the
             # presence counts, as the reference's host math); the masks are built from the
             # device means and only what the package holds comes to the host
-            sums = torch.stack([self.score_sums[i] for i in layers])
-            presence = torch.stack([self.score_presence_sums[i] for i in layers]).clamp_min_(1.0)
-            mean = sums / presence
-            del sums
-            mask_list = _to_host(_build_direct_mean_coverage_masks(list(mean.unbind(0)), cfg))
-            mean_list = std_list = None
-            if include_scores:
-                var = (torch.stack([self.score_sq_sums[i] for i in layers]) / presence - mean.square()).clamp_min_(0.0)
-                mean_list = _to_host(list(mean.unbind(0)))
-                # the square root on the host: torch's device sqrt is not correctly rounded
-                std_list = [torch.sqrt(x) for x in _to_host(list(var.unbind(0)))]
+            mask_list, mean_list, std_list = _device_package_groups(
+                [self.score_sums[i] for i in layers], [self.score_sq_sums[i] for i in layers],
+                [self.score_presence_sums[i] for i in layers], cfg, include_scores, denom_min=1.0)
             for j, layer in enumerate(layers):
                 key = str(layer)
                 if include_scores:

@@ -34,7 +34,7 @@ sys.path.insert(0, str(GOLD))
 from max_pool_cases import CASES, DTYPE, digest, make_inputs  # noqa: E402
 
 sys.path.pop(0)
-from parity_bars import max_block_logit, max_pool_bar  # noqa: E402
+from parity_bars import flips_near_rounding_boundary, max_block_logit, max_pool_bar  # noqa: E402
 FIX = np.load(GOLD / "max_pool.npz")
 CASE_BY_NAME = {c[0]: c for c in CASES}
 
@@ -57,7 +57,7 @@ def test_fixture_lists_every_case():
 
 
 def _randn_bar(got, po, q, k, sm, block, causal, what):
-    max_pool_bar(got, po, max_block_logit(q, k, sm, block, causal), what)
+    max_pool_bar(got, po, max_block_logit(q, k, sm, block, causal), what, qk=(q, k, sm, block, causal))
 
 
 @pytest.mark.parametrize("name", sorted(CASE_BY_NAME))
@@ -70,6 +70,25 @@ def test_oracle_reproduces_reference_fixture(name):
         assert int(d.max()) == 0, int(d.gt(0).sum())
     else:
         _randn_bar(ours, po, q, k, sm, block, causal, name)
+
+
+def test_bar_rejects_a_planted_error_away_from_rounding_boundaries():
+    # A mistake planted in the oracle's map: one entry of an N(0,1) case scaled by 1.008,
+    # inside the 2^ulp(max|R|) - 1 = 1.09% growth the bar allows for boundary flips but far
+    # beyond its 2-ulp ripple.  Its q-block has no row near a rounding boundary, so the
+    # cause check must fail it.
+    q, k, _, po, block, causal, sm, kind = _case("randn_b128_d128")
+    ours = torch_ref.max_pool_map(q, k, sm, block, causal=causal)
+    cand = [(0, h, qb, kb) for h in range(ours.size(1)) for qb in range(ours.size(2)) for kb in range(ours.size(3))]
+    ent = torch.tensor(cand)
+    near = flips_near_rounding_boundary(q, k, sm, block, causal, ent, DTYPE)
+    assert bool(near.any()) and not bool(near.all())   # the check separates entries
+    b, h, qb, kb = cand[int((~near).nonzero()[0])]
+    bad = ours.clone()
+    bad[b, h, qb, kb] = (bad[b, h, qb, kb].double() * 1.008).to(DTYPE)
+    _randn_bar(ours, po, q, k, sm, block, causal, "unplanted")
+    with pytest.raises(AssertionError, match="no row near a rounding boundary"):
+        _randn_bar(bad, po, q, k, sm, block, causal, "planted")
 
 
 @pytest.mark.parametrize("point", ["R", "Po", "sum", "div"])

@@ -39,7 +39,7 @@ def _qk(B, H, Nq, Nk, dtype, seed, sinks=0, sink_scale=8.0, sink_at_end=False):
 
 
 def _max_pool_close(ours, ref, q, k, sm, block=128, causal=False, what=""):
-    max_pool_bar(ours, ref, max_block_logit(q, k, sm, block, causal), what)
+    max_pool_bar(ours, ref, max_block_logit(q, k, sm, block, causal), what, qk=(q, k, sm, block, causal))
 
 
 def _close(ours, ref):
@@ -153,7 +153,7 @@ def test_max_pool_many_key_blocks():
         ref = torch_ref.max_pool_map(q, k, 0.088, causal=causal, query_blocks=sel)
         rows = [r * 128 + i for r in sel for i in range(128) if r * 128 + i < 40000]
         max_pool_bar(ours[:, :, sel], ref, max_block_logit(q, k, 0.088, 128, causal, rows=rows),
-                     what=f"causal={causal}")
+                     what=f"causal={causal}", qk=(q, k, 0.088, 128, causal, sel))
 
 
 def test_attn_with_pooling_api_and_gqa():

@@ -11,6 +11,7 @@ file:line that imports it (e.g. `wanx/runtime/inference.py:23` for the two timin
 
 Also the two timing helpers the Wan inference CLI imports, on hand-built summaries
 (sinkattention/timing.py:103-169)."""
+import ast
 import dataclasses
 import importlib
 import inspect
@@ -28,16 +29,29 @@ def _row_id(row):
     return f"{row['module']}.{row['name']}"
 
 
+def _value(src, module):
+    """A default-value string of the table as a Python value: a literal (ast.literal_eval),
+    or else a bare identifier resolved on the serving module.  Nothing else is evaluated:
+    the strings come from parsing untrusted source."""
+    try:
+        return ast.literal_eval(src)
+    except (ValueError, SyntaxError):
+        pass
+    if not src.isidentifier():
+        raise AssertionError(f"default value {src!r} is neither a literal nor a name")
+    assert hasattr(module, src), f"default value name {src} is not defined on {module.__name__}"
+    return getattr(module, src)
+
+
 def _check_params(obj, exp, module):
     params = list(inspect.signature(obj).parameters.values())
     assert [p.name for p in params] == [e[0] for e in exp]
     assert [p.kind.name for p in params] == [e[1] for e in exp]
-    ns = vars(module)
     for p, (name, _, default_src) in zip(params, exp):
         if default_src is None:
             assert p.default is inspect.Parameter.empty, name
         else:
-            assert p.default == eval(default_src, dict(ns)), name
+            assert p.default == _value(default_src, module), name
 
 
 @pytest.mark.parametrize("row", TABLE, ids=_row_id)
@@ -56,15 +70,14 @@ def test_reference_import_resolves_with_reference_signature(row):
         if "fields" in d:
             fields = {f.name: f for f in dataclasses.fields(obj)}
             assert list(fields) == [f[0] for f in d["fields"]]
-            ns = dict(vars(module))
             for name, default_src in d["fields"]:
                 f = fields[name]
                 if default_src is None:
                     assert f.default is dataclasses.MISSING and f.default_factory is dataclasses.MISSING
                 else:
-                    assert f.default == eval(default_src, ns), name
+                    assert f.default == _value(default_src, module), name
     elif d["kind"] == "constant":
-        assert obj == eval(d["value"], dict(vars(module)))
+        assert obj == _value(d["value"], module)
     else:
         pytest.fail(f"unhandled kind {d['kind']}")
 

@@ -36,16 +36,19 @@ def _outputs(q):
 
 
 def _noalloc(q, k, v, mask):
+    out, lse = _outputs(q)
+    _noalloc_into(q, k, v, mask.to(torch.uint8), out, lse)
+    return out, lse
+
+
+def _noalloc_into(q, k, v, m, out, lse):
     lib = _lib.lib()
     B, H, Nq, D = q.shape
-    out, lse = _outputs(q)
-    m = mask.to(torch.uint8)
     rc = lib.sinkattn_block_sparse_attn_noalloc(
         m.data_ptr(), _lib.strides4(m), q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.dtype_code(q.dtype),
         B, H, Nq, k.shape[2], D, _lib.strides4(q), _lib.strides4(k), _lib.strides4(v),
         out.data_ptr(), _lib.strides4(out), lse.data_ptr(), 1.0 / math.sqrt(D), _lib.stream_ptr(q.device))
     _lib.check(rc, "sinkattn_block_sparse_attn_noalloc")
-    return out, lse
 
 
 def _with_plan(q, k, v, mask):
@@ -106,3 +109,30 @@ def test_noalloc_rejects_plans_beyond_the_static_buffer():
     assert rc < 0
     msg = lib.sinkattn_last_error().decode()
     assert "static plan buffer" in msg and "sinkattn_block_sparse_plan" in msg
+
+
+def test_noalloc_captured_in_a_graph_replays_new_inputs():
+    """After one eager call on the GPU (the static buffer's address is then known), the call
+    is captured with torch.cuda.graph and replayed on new q/k/v/mask contents copied into the
+    captured buffers; every replay must equal plan + forward on the same inputs, bit for bit,
+    with eager work and synchronisations between the replays."""
+    q, k, v, mask = _inputs(1, 3, 1500, torch.bfloat16, seed=4, density=0.35)
+    m = mask.to(torch.uint8)
+    out, lse = _outputs(q)
+    _noalloc_into(q, k, v, m, out, lse)            # eager first call
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _noalloc_into(q, k, v, m, out, lse)
+    torch.cuda.synchronize()
+    for seed in (5, 6, 7):
+        q2, k2, v2, mask2 = _inputs(1, 3, 1500, torch.bfloat16, seed=seed, density=0.2 + 0.1 * (seed - 5))
+        print(f"graph replay seed {seed}", flush=True)
+        q.copy_(q2), k.copy_(k2), v.copy_(v2), m.copy_(mask2.to(torch.uint8))
+        out.fill_(float("nan")), lse.fill_(float("nan"))
+        g.replay()
+        want_o, want_l = _with_plan(q2, k2, v2, mask2)   # eager work between replays
+        torch.cuda.synchronize()
+        assert not torch.isnan(out).any() and not torch.isnan(lse).any()
+        assert _same(out, want_o)
+        assert _same(lse, want_l)
