@@ -87,7 +87,7 @@ def flips_near_rounding_boundary(q: torch.Tensor, k: torch.Tensor, sm_scale: flo
 
 
 def max_pool_bar(got: torch.Tensor, ref: torch.Tensor, r_max: float, what: str = "",
-                 max_row_frac: float = 0.10, max_flip_frac: float = 0.01, qk=None,
+                 max_row_frac: float = 0.08, max_flip_frac: float = 2e-3, qk=None,
                  max_checked: int = 400) -> None:
     """Bar for the max-pool map where q.k is summed in another order than in `ref`.
 
@@ -99,6 +99,10 @@ def max_pool_bar(got: torch.Tensor, ref: torch.Tensor, r_max: float, what: str =
     (one needs a q.k within a few fp32 ulps of a boundary): at most `max_flip_frac` of the
     entries differ by more than the 2-ulp ripple of a row total, and at most `max_row_frac`
     of the rows differ at all.
+
+    The defaults sit just above what the kernels show against the reference's fixtures and
+    the oracle (at most 1 entry of 1024 beyond the ripple and 2 rows of 32 touched, on 16-
+    to 32-block maps).
 
     `qk` = (q, k, sm_scale, block, causal[, query_blocks]): then every entry beyond the 2-ulp
     ripple (up to `max_checked` of them, a seeded sample) must also have the cause above, a

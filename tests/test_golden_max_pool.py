@@ -14,7 +14,9 @@ N(0,1) inputs, both: the fp32 sums q.k are rounded in another order (numpy's BLA
       fixture, this host's BLAS in the oracle, the matrix cores on the GPU), which moves a
       block maximum R across a q.dtype rounding boundary now and then; the bar there is
       `parity_bars.max_pool_bar` (entries within the factor 2^ulp(max |R|) plus two ulps,
-      at most 1% of the entries beyond a 2-ulp ripple, 10% of the rows touched).
+      at most 0.2% of the entries beyond a 2-ulp ripple, 8% of the rows touched, and every
+      entry beyond the ripple explained by a deciding row whose block maximum lies within
+      the fp32 dot-product error of a rounding boundary).
 bf16: the interpreter cannot run the kernel in bf16 (see the fixture script), so bf16 rests
       on the same oracle code, whose bf16 conversion is checked here to round to nearest
       even, and on the GPU-vs-oracle test with the same bar.
