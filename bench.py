@@ -30,6 +30,10 @@ import time
 
 MFMA_BF16_PEAK_TFLOPS = 2516.6
 HBM_PEAK_GBS = 8000.0
+NOMINAL_CLOCK_GHZ = 2.4
+# Shader clock of block_mass_persistent_kernel at the config-2 shape, from rocprofv3
+# --pmc GRBM_GUI_ACTIVE (cycles per dispatch / its duration): profiles/block_mass_pool_wan_c2.md.
+POOL_KERNEL_CLOCK_GHZ = 1.59
 
 # HBM traffic per launch at the default workload (--density 0.20, the seeds below),
 # from rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (KiB per dispatch) scaled by what
@@ -123,6 +127,25 @@ def time_fn(torch, fn, steps, warmup, per_launch=False):
     if per_launch:
         return total, sum(a.elapsed_time(b) for a, b in marks) / steps
     return total
+
+
+def gpu_time_fn(torch, fn, steps, warmup):
+    """Mean GPU time per call of a short, host-heavy call (plans, small kernels): a spin kernel
+    (torch.cuda._sleep) holds the GPU while the host enqueues all `steps` calls, so the
+    interval between the events is the calls' own device time, back to back, without the
+    host's enqueue time showing as idle gaps."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(4e7))
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
 
 
 def cpu_baseline(torch, q, k, v, mask, n_qblocks, total_flops_layer):
@@ -238,6 +261,48 @@ def cpu_calibration_baseline(torch, ops, q, k, gpu_pool_ms, gpu_mask_us):
     }
 
 
+def valu_roof(torch, dev, pool_ms, scores):
+    """The exact block-mass pass against its VALU roof.  Per score the kernel issues one
+    v_fma_f32, one v_exp_f32 and one v_add_f32 beside the MFMA work; the probe kernel
+    (sinkattn_amd/csrc/probe/valu_mix.hip) issues exactly that mix at the pooling kernel's
+    occupancy and gives the rate a CU retires it at, per shader clock (clock from the
+    probe's own s_memtime / s_memrealtime stamps).  roof_ms = scores / (rate * CUs * clock)
+    at the nominal 2.4 GHz and at the pooling kernel's profiled clock."""
+    import ctypes
+    from sinkattn_amd import build as sbuild
+    lib = ctypes.CDLL(str(sbuild.PROBE_PATH))
+    lib.sinkattn_probe_valu_mix.restype = ctypes.c_int
+    lib.sinkattn_probe_valu_mix.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_void_p]
+    chains = int(lib.sinkattn_probe_chains())
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    blocks, reps = 3 * cus, 4096
+    sink = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    stamps = torch.zeros(blocks * 4 * 3, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def run():
+        rc = lib.sinkattn_probe_valu_mix(blocks, reps, 0.1275, sink.data_ptr(), stamps.data_ptr(), stream)
+        if rc != 0:
+            raise RuntimeError(f"valu probe launch failed: {rc}")
+
+    ms = time_fn(torch, run, 5, 2)
+    st = stamps.view(-1, 3).cpu().double()
+    clock_hz = float((st[:, 0] / ((st[:, 2] - st[:, 1]) * 1e-8)).mean())
+    n = blocks * 256 * reps * chains
+    rate = n / (ms * 1e-3) / clock_hz / cus        # scores per shader clock per CU
+    roof_nom = scores / (rate * cus * NOMINAL_CLOCK_GHZ * 1e9) * 1e3
+    roof_k = scores / (rate * cus * POOL_KERNEL_CLOCK_GHZ * 1e9) * 1e3
+    return {"bound": "valu", "mix_per_score": "v_fma_f32 + v_exp_f32 + v_add_f32",
+            "scores_per_launch": scores,
+            "probe_scores_per_clock_per_cu": round(rate, 2), "probe_clock_ghz": round(clock_hz / 1e9, 3),
+            "roof_ms_at_nominal_clock": round(roof_nom, 3), "frac_at_nominal_clock": round(roof_nom / pool_ms, 4),
+            "kernel_clock_ghz_profiled": POOL_KERNEL_CLOCK_GHZ,
+            "roof_ms_at_kernel_clock": round(roof_k, 3), "frac_at_kernel_clock": round(roof_k / pool_ms, 4),
+            "note": "fraction = VALU-roof time / measured pooling time; the clock of the pooling kernel "
+                    "comes from rocprofv3 GRBM_GUI_ACTIVE (profiles/block_mass_pool_wan_c2.md)"}
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -275,7 +340,7 @@ def main():
 
     if args.only == "fa4":  # the config-4 (Z-Image) attention alone
         del q, k, v
-        qz, kz, vz, _, _, mz = zimage_inputs(torch, dev, sa)
+        qz, kz, vz, _, _, mz, _ = zimage_inputs(torch, dev, sa)
         zplan = ops.block_sparse_plan(mz)
         kernel_call = lambda: ops.block_sparse_attention(qz, kz, vz, zplan)  # noqa: E731
     if args.only != "all":
@@ -356,6 +421,7 @@ def main():
                           "mfma_frac": round(pool_flops / (pms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
                           "traffic": traffic_bytes("pool"),
                           "kernel": "sa::block_mass_persistent_kernel<0> (bf16)"}
+        out["pooling"]["valu_roof"] = valu_roof(torch, dev, pms, float(B * H * N * N))
         # the "triton" pooling mode (attn_with_pooling's row-normalised max-pool map)
         mms = time_fn(torch, lambda: ops.max_pool_scores(q, k, 1.0 / math.sqrt(D)), 3, 1)
         out["pooling"]["max_pool_ms"] = round(mms, 3)
@@ -416,9 +482,15 @@ def main():
         scores = scores / scores.sum(-1, keepdim=True)
         mus = time_fn(torch, lambda: ops.coverage_mask(scores, 0.85, True), 10, 2) * 1e3
         out["coverage_mask_us"] = round(mus, 1)
-        # a mask the drop-in has not seen yet costs one plan (lists + launch order) first
-        plus = time_fn(torch, lambda: ops.block_sparse_plan(mask), 10, 3) * 1e3
+        # a mask the drop-in has not seen yet costs one plan (lists + launch order) first;
+        # device time per plan, back to back
+        plus = gpu_time_fn(torch, lambda: ops.block_sparse_plan(mask), 10, 3) * 1e3
         out["plan_us"] = round(plus, 1)
+        # the same counts in a fresh tensor: lists rebuilt, launch order from the order cache
+        oc = torch.zeros(ops.order_cache_ints(B, H, 256, 4), dtype=torch.int32, device=dev)
+        ops.block_sparse_plan(mask, oc, 4)
+        pcus = gpu_time_fn(torch, lambda: ops.block_sparse_plan(mask, oc, 4), 10, 3) * 1e3
+        out["plan_order_cached_us"] = round(pcus, 1)
         out["zimage_layer"] = zimage_layer(torch, dev, ops, sa, args)
         out["wan_calibration_pass"] = wan_calibration(torch, dev, sa)
         out["wan_attention_stack"] = wan_stack(torch, dev, ops, q, k, v)
@@ -444,16 +516,17 @@ def zimage_inputs(torch, dev, sa):
     # exact block mass: the Z-Image calibration CLI's default (zimg/offline/calibrate_sink_sparse.py:109)
     cfg = zr.build_zimg_sink_config(config_overrides={"pooling_mode": "exact"})
     scores = sa._compute_block_scores(q, k, v, cfg).mean(0)
-    mask = sa._build_direct_mean_coverage_mask(scores, cfg)
-    mask = zr._force_text_dense_runtime_mask(mask, image_blocks=128, current_text_blocks=4)[None]
-    return q, k, v, cfg, scores, mask
+    pkg_mask = sa._build_direct_mean_coverage_mask(scores, cfg)
+    mask = zr._force_text_dense_runtime_mask(pkg_mask, image_blocks=128, current_text_blocks=4)[None]
+    return q, k, v, cfg, scores, mask, pkg_mask
 
 
 def zimage_layer(torch, dev, ops, sa, args):
     """Z-Image-Turbo 2048x2048 layer (config 4): exact pooling -> coverage-0.85 mask ->
     sparse attention with the text rows and columns forced dense, as the Z-Image runtime
     runs it."""
-    q, k, v, cfg, scores, mask = zimage_inputs(torch, dev, sa)
+    from sinkattn_amd import zimage_runtime as zr
+    q, k, v, cfg, scores, mask, pkg_mask = zimage_inputs(torch, dev, sa)
     B, H, N, D = (int(x) for x in q.shape)
     pms = time_fn(torch, lambda: sa._compute_block_scores(q, k, v, cfg), 3, 1)
     mus = time_fn(torch, lambda: sa._build_direct_mean_coverage_mask(scores, cfg), 10, 2) * 1e3
@@ -464,13 +537,46 @@ def zimage_layer(torch, dev, ops, sa, args):
     ams = time_fn(torch, lambda: ops.block_sparse_attention(q, k, v, plan), args.steps, args.warmup)
     dms = time_fn(torch, lambda: ops.block_sparse_attention(q, k, v, dplan), 3, 1)
     pool_flops = 2.0 * B * H * N * N * D
+
+    # The reference's own Z-Image processor (zimg/runtime/sink_sparse_zimage.py:513-538) builds
+    # the runtime mask afresh on every call (slice of the layer's package mask, text blocks
+    # forced dense, a new tensor) and hands it to the drop-in with return_lse=False (static
+    # mode).  Timed as that whole call sequence, beside the same drop-in call on a cached mask
+    # object and the mask ops alone.
+    pkg = pkg_mask.to(dev)
+
+    def runtime_mask():
+        rm = zr._slice_runtime_sink_mask(pkg, image_blocks=128, current_text_blocks=4, total_blocks=132)
+        return zr._force_text_dense_runtime_mask(rm, image_blocks=128, current_text_blocks=4).unsqueeze(0)
+
+    fresh_ms = time_fn(torch, lambda: sa._block_sparse_attn(q, k, v, runtime_mask(), return_lse=False),
+                       args.steps, args.warmup)
+    cached_ms = time_fn(torch, lambda: sa._block_sparse_attn(q, k, v, mask, return_lse=False),
+                        args.steps, args.warmup)
+    # the drop-in's own part: a mask tensor it has not seen (new object, same content) per call
+    fresh = [mask.clone() for _ in range(args.steps + args.warmup)]
+    it = iter(fresh)
+    tensor_ms = time_fn(torch, lambda: sa._block_sparse_attn(q, k, v, next(it), return_lse=False),
+                        args.steps, args.warmup)
+    del fresh
+    mops_us = gpu_time_fn(torch, runtime_mask, 20, 5) * 1e3
     return {"pooling_ms": round(pms, 3), "pooling_tflops": round(pool_flops / (pms * 1e-3) / 1e12, 2),
             "mask_us": round(mus, 1), "mask_density": round(mask.float().mean().item(), 4),
             "attn_ms": round(ams, 4), "attn_tflops": round(flops / (ams * 1e-3) / 1e12, 2),
             "attn_frac": round(flops / (ams * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
             "dense_same_kernel_ms": round(dms, 3),
             "dense_same_kernel_tflops": round(dense_flops / (dms * 1e-3) / 1e12, 2),
-            "sparse_over_dense_time": round(ams / dms, 4)}
+            "sparse_over_dense_time": round(ams / dms, 4),
+            "reference_processor_fresh_mask": {
+                "call_ms": round(fresh_ms, 4), "cached_mask_call_ms": round(cached_ms, 4),
+                "new_mask_tensor_call_ms": round(tensor_ms, 4),
+                "new_mask_tensor_over_cached_call": round(tensor_ms / cached_ms - 1.0, 4),
+                "runtime_mask_ops_us": round(mops_us, 1),
+                "call_over_cached_call": round(fresh_ms / cached_ms - 1.0, 4),
+                "note": "call: the reference processor's slice + force-text-dense of the package mask (the "
+                        "reference's torch ops, runtime_mask_ops_us of device time) + _block_sparse_attn("
+                        "return_lse=False); new_mask_tensor: the drop-in alone on a mask object it has not "
+                        "seen (lists rebuilt, launch order from the launch-order cache)"}}
 
 
 def wan_calibration(torch, dev, sa, layers=30):
@@ -512,12 +618,13 @@ def wan_calibration(torch, dev, sa, layers=30):
             "note": "wall time of record() x 30 + build_package() after one untimed warm-up layer, inputs resident in HBM"}
 
 
-def wan_stack(torch, dev, ops, q, k, v, layers=30, steps=50, dense_steps=5):
+def wan_stack(torch, dev, ops, q, k, v, layers=30, steps=50, dense_steps=50):
     """Full Wan denoise attention stack: 30 layers with per-(layer, head)
     seeded densities in [5%, 60%] (one fully dense head per layer), the masks static across
     the 50 steps as the runtime's are.  Sparse: the whole 30 x 50 loop of drop-in calls
     (`_block_sparse_attn`, cached plans) timed as one region.  Dense: the same loop with
-    all-true masks over `dense_steps` steps, scaled to 50 (labelled as extrapolated)."""
+    all-true masks, all 50 steps timed as one region (fewer steps are scaled to 50 and
+    labelled as extrapolated)."""
     from sinkattn_amd import sparse_attention as sa
 
     B, H = int(q.shape[0]), int(q.shape[1])
@@ -561,9 +668,10 @@ def wan_stack(torch, dev, ops, q, k, v, layers=30, steps=50, dense_steps=5):
             "sparse_s": round(sparse_ms / 1e3, 3),
             "sparse_s_note": f"measured: {layers} layers x {steps} steps of drop-in calls as one timed region",
             "dense_s": round(dense_s, 3),
-            "dense_s_extrapolated": True,
-            "dense_s_note": (f"measured {layers} layers x {dense_steps} steps with all-true masks "
-                             f"({dense_subset_ms / 1e3:.3f} s), x{steps // dense_steps}"),
+            "dense_s_extrapolated": dense_steps < steps,
+            "dense_s_note": (f"measured: {layers} layers x {dense_steps} steps with all-true masks as one timed "
+                             f"region ({dense_subset_ms / 1e3:.3f} s)"
+                             + (f", x{steps / dense_steps:g}" if dense_steps < steps else "")),
             "sparse_over_dense_time": round(sparse_ms / 1e3 / dense_s, 4),
             "tflops": round(flops_sum * steps / (sparse_ms * 1e-3) / 1e12, 2),
             "mean_density": round(sum(dens) / len(dens), 4)}

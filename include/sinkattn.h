@@ -12,7 +12,8 @@
  * sinkattn_block_sparse_attn_noalloc (end of this file): it keeps its plan in one static
  * device array per GPU (SINKATTN_NOALLOC_SCRATCH_BYTES = 32 MiB, reserved on every GPU
  * that loads this library, whether or not that entry point is called), so calls of it that
- * overlap on one GPU race.
+ * overlap on one GPU race.  sinkattn_block_sparse_plan_cached keeps state only in the
+ * launch-order cache buffer its caller passes (calls sharing one buffer must be ordered).
  *
  * Tensor conventions.  A "BHSD" operand is addressed as
  *     base[b*s[0] + h*s[1] + n*s[2] + d*s[3]]   with s[3] == 1,
@@ -40,7 +41,8 @@ enum sinkattn_dtype { SINKATTN_BF16 = 0, SINKATTN_F16 = 1, SINKATTN_F32 = 2 };
 const char* sinkattn_last_error(void);
 
 /* ABI version of this library (bumped on any change of a signature or of a buffer's
- * contract; 3: the order buffer of a plan also holds its chunk table). */
+ * contract; 3: the order buffer of a plan also holds its chunk table; 4: plans with a
+ * launch-order cache). */
 int sinkattn_abi_version(void);
 
 /* ------------------------------------------------------------------------------------
@@ -64,6 +66,31 @@ int sinkattn_block_sparse_plan(const uint8_t* mask, const int64_t mask_strides[4
                                int64_t B, int64_t H, int64_t nqb, int64_t nkb,
                                int32_t* counts, int32_t* idx, int32_t* order,
                                void* stream);
+
+/* ------------------------------------------------------------------------------------
+ * Block-sparse plan with a launch-order cache.
+ *
+ * Replaces the same hand-off as sinkattn_block_sparse_plan, for callers that hand the
+ * forward a freshly built mask tensor on every call, as the reference's Z-Image processor
+ * does (zimg/runtime/sink_sparse_zimage.py:513-538: `_slice_runtime_sink_mask` +
+ * `_force_text_dense_runtime_mask` per sample per call).  The lists and counts are always
+ * built from `mask`; the launch order, which depends only on the shape and the per-row
+ * tile counts, is copied from `order_cache` when an earlier plan of this shape had tile
+ * counts with the same 64-bit hash, and otherwise ranked as in sinkattn_block_sparse_plan
+ * and then stored in the cache (round robin over `cache_entries` entries).  Results equal
+ * sinkattn_block_sparse_plan's; a hash collision could only give a valid but less balanced
+ * launch order (every order of a shape lists the same q-blocks once each).
+ * order_cache: int32 buffer of sinkattn_block_sparse_order_cache_ints(B, H, nqb, entries)
+ * ints, zero-filled before its first use, kept for one shape (B, H, nqb) and used by calls
+ * ordered on one stream (calls that share a cache concurrently race); 1 <= entries <= 4096.
+ * ---------------------------------------------------------------------------------- */
+int64_t sinkattn_block_sparse_order_cache_ints(int64_t B, int64_t H, int64_t nqb,
+                                               int64_t entries);
+int sinkattn_block_sparse_plan_cached(const uint8_t* mask, const int64_t mask_strides[4],
+                                      int64_t B, int64_t H, int64_t nqb, int64_t nkb,
+                                      int32_t* counts, int32_t* idx, int32_t* order,
+                                      int32_t* order_cache, int64_t cache_entries,
+                                      void* stream);
 
 /* ------------------------------------------------------------------------------------
  * Block-sparse flash-attention forward, 128x128 tiles.

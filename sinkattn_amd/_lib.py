@@ -32,6 +32,11 @@ SIGNATURES = {
         ctypes.c_int,
         [_c_p, _c_i64_4, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p],
     ),
+    "sinkattn_block_sparse_order_cache_ints": (ctypes.c_int64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "sinkattn_block_sparse_plan_cached": (
+        ctypes.c_int,
+        [_c_p, _c_i64_4, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p],
+    ),
     "sinkattn_block_sparse_fwd": (
         ctypes.c_int,
         [_c_p, _c_p, _c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
@@ -105,7 +110,7 @@ class SinkAttnError(RuntimeError):
 
 # Version of the entry-point signatures declared in include/sinkattn.h (raised whenever an
 # existing signature changes).
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 def load_library() -> ctypes.CDLL:

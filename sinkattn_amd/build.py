@@ -2,8 +2,10 @@
 
     python -m sinkattn_amd.build          # or: python sinkattn_amd/build.py
 
-Objects go to sinkattn_amd/_build/, the library to sinkattn_amd/libsinkattn.so.
-All device code is compiled with packed-fp32 instructions disabled.
+Objects go to sinkattn_amd/_build/, the library to sinkattn_amd/libsinkattn.so, and the
+measurement probe bench.py uses (csrc/probe/, not part of the library) to
+sinkattn_amd/libsinkattn_probe.so.  All device code is compiled with packed-fp32
+instructions disabled.
 """
 from __future__ import annotations
 
@@ -18,6 +20,8 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libsinkattn.so"
+PROBE_PATH = PKG_DIR / "libsinkattn_probe.so"
+PROBE_SOURCES = ["probe/valu_mix.hip"]
 ARCH = os.environ.get("SINKATTN_ARCH", "gfx950")
 
 SOURCES = [
@@ -50,7 +54,7 @@ def _hipcc() -> str:
 
 
 def _compile(src: str) -> Path:
-    obj = BUILD_DIR / (Path(src).stem + ".o")
+    obj = BUILD_DIR / (src.replace("/", "_").rsplit(".", 1)[0] + ".o")
     cmd = [_hipcc(), *COMMON_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
@@ -64,18 +68,24 @@ def _compile(src: str) -> Path:
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    BUILD_DIR.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as pool:
-        objs = list(pool.map(_compile, SOURCES))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+def _link(objs, path: Path) -> None:
+    tmp = path.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, path)
+
+
+def build(verbose: bool = True) -> Path:
+    BUILD_DIR.mkdir(exist_ok=True)
+    srcs = SOURCES + PROBE_SOURCES
+    with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as pool:
+        objs = list(pool.map(_compile, srcs))
+    _link(objs[: len(SOURCES)], LIB_PATH)
+    _link(objs[len(SOURCES):], PROBE_PATH)
     if verbose:
-        print(f"built {LIB_PATH}")
+        print(f"built {LIB_PATH} and {PROBE_PATH.name}")
     return LIB_PATH
 
 

@@ -769,6 +769,39 @@ constexpr int kPlanWaves = kPlanThreads / 64;
 // cost sum per XCD (low, high word), [24] outliers taken out (1) or not (0), then per chunk
 // ch [32 + 2ch] its first slot along its XCD's sequence and [33 + 2ch] its XCD.
 constexpr int kMetaHead = 32;
+// [25] 1 when the launch slots were copied from the launch-order cache (the chunk pass then
+// has nothing to do), [26], [27] the hash of the plan's tile counts (low, high word).
+constexpr int kMetaCopied = 25, kMetaHashLo = 26, kMetaHashHi = 27;
+
+// Launch-order cache: int32 [kCacheHead + entries * (kCacheEntryHead + S)], S =
+// plan_order_slots() of the shape, zero-filled by its owner before first use and used by
+// one stream at a time.  Head: [0] the next entry to fill, [1] chunk-pass groups done (the
+// last one inserts the finished order and sets it back to zero).  Entry: [0] 1 when filled,
+// [1], [2] the hash of its tile counts, then the S ints of its order buffer.  The launch
+// order depends only on the shape and the tile counts, so a plan whose counts hash like a
+// filled entry's takes that entry's order instead of ranking the chunks again.  A hash
+// collision can only cost balance, never correctness: every order of a shape is a
+// permutation of the same q-blocks.
+constexpr int kCacheHead = 4, kCacheEntryHead = 4;
+
+// SplitMix64's output function (Steele, Lea, Flood 2014): a 64-bit mixer.
+__device__ __forceinline__ uint64_t mix64(uint64_t x) {
+  x ^= x >> 30;
+  x *= 0xbf58476d1ce4e5b9ull;
+  x ^= x >> 27;
+  x *= 0x94d049bb133111ebull;
+  return x ^ (x >> 31);
+}
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, off, 64);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
+    v += ((uint64_t)hi << 32) | lo;
+  }
+  return v;
+}
 
 __host__ __device__ inline int chunk_size(const ChunkLayout& L, int nqb, int ch) {
   const int C = ch < L.nw ? L.Cw : L.Cs;
@@ -812,11 +845,15 @@ __global__ __launch_bounds__(kPlanThreads) void plan_order_kernel(PlanArgs a) {
   __shared__ int outl[kMaxOutliers], outl_c[kMaxOutliers];
   __shared__ uint8_t outl_x[kMaxOutliers];
   __shared__ int16_t nonout[kMaxChunks];
+  __shared__ unsigned long long hash_part[kPlanWaves];
+  __shared__ int hit;
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wv = tid >> 6;
   const ChunkLayout L = chunk_layout(a.rows / a.nqb, a.nqb);
   const int nch = L.nw + L.ns;
   const int total = L.slots_per_xcd() * kXcds;
+  const int S = total + kMetaHead + 2 * nch;  // ints of the order buffer
+  int32_t* meta = a.order + total;
   if constexpr (STAGED) {
     for (int base = 0; base < a.rows; base += 8 * kPlanThreads) {
       int v[8];
@@ -832,6 +869,45 @@ __global__ __launch_bounds__(kPlanThreads) void plan_order_kernel(PlanArgs a) {
       }
     }
   }
+  auto counts = [&](int row) __attribute__((always_inline)) {
+    if constexpr (STAGED) return cnt_lds[row];
+    else return a.counts[row];
+  };
+  // With a launch-order cache: the hash of the tile counts (a wrapping sum of one mixed
+  // word per row, so any thread may take any row), then the first filled entry with that
+  // hash, whose order is copied.
+  uint64_t hash = 0;
+  if (a.cache != nullptr) {
+    __syncthreads();  // counts staged
+    uint64_t hs = 0;
+    for (int row = tid; row < a.rows; row += kPlanThreads)
+      hs += mix64(((uint64_t)(uint32_t)row << 32) | (uint32_t)counts(row));
+    hs = wave_sum_u64(hs);
+    if (lane == 0) hash_part[wv] = hs;
+    __syncthreads();
+    hash = mix64(((uint64_t)(uint32_t)a.rows << 32) | (uint32_t)a.nqb);
+    for (int w = 0; w < kPlanWaves; ++w) hash += hash_part[w];
+    if (wv == 0) {
+      int found = -1;
+      for (int e0 = 0; e0 < a.cache_entries && found < 0; e0 += 64) {
+        const int e = e0 + lane;
+        bool m = false;
+        if (e < a.cache_entries) {
+          const int32_t* eh = a.cache + kCacheHead + (int64_t)e * (kCacheEntryHead + S);
+          m = eh[0] == 1 && (uint32_t)eh[1] == (uint32_t)hash && (uint32_t)eh[2] == (uint32_t)(hash >> 32);
+        }
+        const uint64_t b = __ballot(m);
+        if (b != 0) found = e0 + __ffsll((unsigned long long)b) - 1;
+      }
+      if (lane == 0) hit = found;
+    }
+    __syncthreads();
+    if (hit >= 0) {
+      const int32_t* src = a.cache + kCacheHead + (int64_t)hit * (kCacheEntryHead + S) + kCacheEntryHead;
+      for (int i = tid; i < S; i += kPlanThreads) a.order[i] = i == total + kMetaCopied ? 1 : src[i];
+      return;
+    }
+  }
   for (int i = tid; i < total; i += kPlanThreads) a.order[i] = -1;
   if (tid < kXcds) {
     xsum[tid] = 0;
@@ -839,10 +915,6 @@ __global__ __launch_bounds__(kPlanThreads) void plan_order_kernel(PlanArgs a) {
   }
   if (tid == 0) nlist = 0;
   __syncthreads();
-  auto counts = [&](int row) __attribute__((always_inline)) {
-    if constexpr (STAGED) return cnt_lds[row];
-    else return a.counts[row];
-  };
   // chunk costs: one wave per chunk, its lanes striding over the chunk's q-blocks
   for (int ch = wv; ch < nch; ch += kPlanWaves) {
     int bh, j, C;
@@ -981,7 +1053,6 @@ __global__ __launch_bounds__(kPlanThreads) void plan_order_kernel(PlanArgs a) {
     }
   }
   __syncthreads();
-  int32_t* meta = a.order + total;
   if (tid < kXcds) {  // offsets along each XCD's chunk sequence
     const int x = tid;
     int off = use_out ? nout[x] : 0;
@@ -995,7 +1066,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_order_kernel(PlanArgs a) {
     meta[8 + 2 * x] = (int32_t)(xsum[x] & 0xffffffffull);
     meta[9 + 2 * x] = (int32_t)(xsum[x] >> 32);
   }
-  if (tid == 0) meta[24] = use_out ? 1 : 0;
+  if (tid == 0) {
+    meta[24] = use_out ? 1 : 0;
+    meta[kMetaCopied] = 0;
+    meta[kMetaHashLo] = (int32_t)(uint32_t)hash;
+    meta[kMetaHashHi] = (int32_t)(uint32_t)(hash >> 32);
+  }
   for (int ch = tid; ch < nch; ch += kPlanThreads) meta[kMetaHead + 2 * ch + 1] = xcd[ch];
   // Outliers: rank among the XCD's outliers by cost desc, then row asc.
   if (use_out) {
@@ -1022,7 +1098,9 @@ __global__ __launch_bounds__(64) void plan_chunk_sort_kernel(PlanArgs a) {
   const int lane = (int)threadIdx.x;
   const int ch = (int)blockIdx.x;
   const ChunkLayout L = chunk_layout(a.rows / a.nqb, a.nqb);
-  const int32_t* meta = a.order + L.slots_per_xcd() * kXcds;
+  const int total = L.slots_per_xcd() * kXcds;
+  const int32_t* meta = a.order + total;
+  if (a.cache != nullptr && meta[kMetaCopied] == 1) return;  // slots copied from the cache
   int bh, j, C;
   chunk_head(L, ch, bh, j, C);
   const int S = (a.nqb - j + C - 1) / C;
@@ -1054,6 +1132,28 @@ __global__ __launch_bounds__(64) void plan_chunk_sort_kernel(PlanArgs a) {
   for (int u = 0; u < 4; ++u) {
     const int k = lane + 64 * u;
     if (key[u] >= 0) a.order[(off + rank[u]) * kXcds + x] = bh * a.nqb + j + k * C;
+  }
+  if (a.cache == nullptr) return;
+  // The last group to finish copies the whole order buffer into the cache entry to fill next
+  // (device-scope fences around the completion count; the other groups' slots are read with
+  // agent-scope loads).
+  __threadfence();
+  int last = 0;
+  if (lane == 0) last = atomicAdd(a.cache + 1, 1) == (int)gridDim.x - 1;
+  last = __shfl(last, 0, 64);
+  if (!last) return;
+  __threadfence();
+  const int ints = total + kMetaHead + 2 * (L.nw + L.ns);  // of the order buffer
+  const int e = __hip_atomic_load(a.cache, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) % a.cache_entries;
+  int32_t* ent = a.cache + kCacheHead + (int64_t)e * (kCacheEntryHead + ints);
+  for (int i = lane; i < ints; i += 64)
+    ent[kCacheEntryHead + i] = __hip_atomic_load(a.order + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) {
+    ent[0] = 1;
+    ent[1] = meta[kMetaHashLo];
+    ent[2] = meta[kMetaHashHi];
+    a.cache[0] = (e + 1) % a.cache_entries;
+    a.cache[1] = 0;
   }
 }
 
@@ -1096,6 +1196,10 @@ int plan_order_slots(int rows, int nqb) {
   if (slots == 0 || !chunked_order(rows, nqb)) return slots;
   const ChunkLayout L = chunk_layout(rows / nqb, nqb);
   return slots + kMetaHead + 2 * (L.nw + L.ns);
+}
+
+int64_t plan_order_cache_ints(int rows, int nqb, int entries) {
+  return kCacheHead + (int64_t)entries * (kCacheEntryHead + plan_order_slots(rows, nqb));
 }
 
 hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream) {

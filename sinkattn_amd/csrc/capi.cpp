@@ -71,22 +71,29 @@ extern "C" {
 
 const char* sinkattn_last_error(void) { return g_last_error.c_str(); }
 
-int sinkattn_abi_version(void) { return 3; }
+int sinkattn_abi_version(void) { return 4; }
 
 int64_t sinkattn_block_sparse_order_slots(int64_t B, int64_t H, int64_t nqb) {
   if (B <= 0 || H <= 0 || nqb <= 0 || B * H * nqb > kMaxInt) return 0;
   return sa::plan_order_slots((int)(B * H * nqb), (int)nqb);
 }
 
-int sinkattn_block_sparse_plan(const uint8_t* mask, const int64_t mask_strides[4], int64_t B,
-                               int64_t H, int64_t nqb, int64_t nkb, int32_t* counts,
-                               int32_t* idx, int32_t* order, void* stream) {
+int64_t sinkattn_block_sparse_order_cache_ints(int64_t B, int64_t H, int64_t nqb, int64_t entries) {
+  if (B <= 0 || H <= 0 || nqb <= 0 || B * H * nqb > kMaxInt || entries < 1 || entries > 4096) return 0;
+  return sa::plan_order_cache_ints((int)(B * H * nqb), (int)nqb, (int)entries);
+}
+
+static int plan_impl(const uint8_t* mask, const int64_t mask_strides[4], int64_t B, int64_t H,
+                     int64_t nqb, int64_t nkb, int32_t* counts, int32_t* idx, int32_t* order,
+                     int32_t* cache, int64_t entries, void* stream) {
   if (B < 0 || H < 0 || nqb < 0 || nkb < 0) return fail("plan: negative size");
   const int64_t rows = B * H * nqb;
   if (rows > kMaxInt || nkb > 8192) return fail("plan: too many rows or key blocks (nkb <= 8192)");
   if (rows == 0) return 0;
   if (mask == nullptr || mask_strides == nullptr || counts == nullptr || idx == nullptr)
     return fail("plan: null pointer");
+  if (cache != nullptr && (order == nullptr || entries < 1 || entries > 4096))
+    return fail("plan: a launch-order cache needs an order buffer and 1..4096 entries");
   sa::PlanArgs a{};
   a.mask = mask;
   for (int i = 0; i < 4; ++i) a.ms[i] = mask_strides[i];
@@ -97,7 +104,24 @@ int sinkattn_block_sparse_plan(const uint8_t* mask, const int64_t mask_strides[4
   a.counts = counts;
   a.idx = idx;
   a.order = order;
+  a.cache = cache;
+  a.cache_entries = cache != nullptr ? (int)entries : 0;
   return hip_status(sa::launch_block_sparse_plan(a, (hipStream_t)stream), "plan launch");
+}
+
+int sinkattn_block_sparse_plan(const uint8_t* mask, const int64_t mask_strides[4], int64_t B,
+                               int64_t H, int64_t nqb, int64_t nkb, int32_t* counts,
+                               int32_t* idx, int32_t* order, void* stream) {
+  return plan_impl(mask, mask_strides, B, H, nqb, nkb, counts, idx, order, nullptr, 0, stream);
+}
+
+int sinkattn_block_sparse_plan_cached(const uint8_t* mask, const int64_t mask_strides[4], int64_t B,
+                                      int64_t H, int64_t nqb, int64_t nkb, int32_t* counts,
+                                      int32_t* idx, int32_t* order, int32_t* order_cache,
+                                      int64_t cache_entries, void* stream) {
+  if (order_cache == nullptr) return fail("plan_cached: null launch-order cache");
+  return plan_impl(mask, mask_strides, B, H, nqb, nkb, counts, idx, order, order_cache, cache_entries,
+                   stream);
 }
 
 }  // extern "C"

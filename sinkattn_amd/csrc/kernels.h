@@ -13,6 +13,10 @@ struct PlanArgs {
   int32_t* counts;
   int32_t* idx;
   int32_t* order;
+  // Launch-order cache (nullptr: none): orders of earlier plans of this shape, keyed by a
+  // hash of their tile counts; see plan_order_cache_ints().
+  int32_t* cache;
+  int cache_entries;
 };
 
 struct FwdArgs {
@@ -104,6 +108,7 @@ struct QkPrepArgs {
 
 constexpr int kXcds = 8;  // gfx950: work-group i is dispatched to XCD i % 8
 int plan_order_slots(int rows, int nqb);
+int64_t plan_order_cache_ints(int rows, int nqb, int entries);
 hipError_t launch_block_sparse_plan(const PlanArgs& a, hipStream_t stream);
 hipError_t launch_block_sparse_fwd(const FwdArgs& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream);

@@ -65,8 +65,12 @@ class BlockSparsePlan:
         return self.counts.sum()
 
 
-def block_sparse_plan(block_mask: torch.Tensor) -> BlockSparsePlan:
-    """Turn a bool [B, H, nqb, nkb] mask into the kernel's lists (one small launch)."""
+def block_sparse_plan(block_mask: torch.Tensor, order_cache: Optional[torch.Tensor] = None,
+                      cache_entries: int = 0) -> BlockSparsePlan:
+    """Turn a bool [B, H, nqb, nkb] mask into the kernel's lists and launch order.  With
+    `order_cache` (int32, order_cache_ints(B, H, nqb, cache_entries) entries, zero-filled
+    when new, one shape, used on one stream) the launch order is copied from an earlier
+    plan whose tile counts hash alike instead of being ranked again."""
     _require_cuda("block_sparse_plan", block_mask)
     if block_mask.dim() != 4:
         raise ValueError(f"block mask must be [B, H, nqb, nkb], got {tuple(block_mask.shape)}")
@@ -83,21 +87,50 @@ def block_sparse_plan(block_mask: torch.Tensor) -> BlockSparsePlan:
                         device=dev)
     with torch.cuda.device(dev):
         st = _lib.strides4(m)
-        _lib.check(
-            L.sinkattn_block_sparse_plan(
-                m.data_ptr(), st, B, H, nqb, nkb, counts.data_ptr(), idx.data_ptr(),
-                order.data_ptr(), _lib.stream_ptr(dev),
-            ),
-            "block_sparse_plan",
-        )
+        if order_cache is None:
+            rc = L.sinkattn_block_sparse_plan(m.data_ptr(), st, B, H, nqb, nkb, counts.data_ptr(),
+                                              idx.data_ptr(), order.data_ptr(), _lib.stream_ptr(dev))
+        else:
+            need = int(L.sinkattn_block_sparse_order_cache_ints(B, H, nqb, int(cache_entries)))
+            if (order_cache.dtype != torch.int32 or order_cache.device != dev or not order_cache.is_contiguous()
+                    or order_cache.numel() < need or need <= 0):
+                raise ValueError(f"order_cache must be a contiguous int32 tensor of {need} entries on {dev}")
+            rc = L.sinkattn_block_sparse_plan_cached(m.data_ptr(), st, B, H, nqb, nkb, counts.data_ptr(),
+                                                     idx.data_ptr(), order.data_ptr(), order_cache.data_ptr(),
+                                                     int(cache_entries), _lib.stream_ptr(dev))
+        _lib.check(rc, "block_sparse_plan")
     return BlockSparsePlan(counts, idx, order, (B, H, nqb, nkb))
 
 
+def order_cache_ints(B: int, H: int, nqb: int, entries: int) -> int:
+    return int(_lib.lib().sinkattn_block_sparse_order_cache_ints(B, H, nqb, entries))
+
+
 class _PlanCache:
-    """Plans keyed by mask tensor identity and version (runtime masks are cached objects)."""
+    """Plans keyed by mask tensor identity and version (runtime masks are cached objects).
+
+    A mask tensor not seen before (callers such as the reference's Z-Image processor build a
+    fresh one per call) gets a new plan: its lists are always built from the mask, and its
+    launch order comes from a device-side launch-order cache per (shape, device, stream)
+    when an earlier plan of that shape had tile counts that hash alike, so only the first
+    call of each distinct count pattern ranks the order (no host synchronisation either
+    way)."""
+
+    ORDER_CACHE_ENTRIES = 64
 
     def __init__(self) -> None:
         self._entries: Dict[int, tuple] = {}
+        self._order_caches: Dict[tuple, torch.Tensor] = {}
+
+    def order_cache(self, mask: torch.Tensor) -> torch.Tensor:
+        B, H, nqb, _ = (int(x) for x in mask.shape)
+        key = (B, H, nqb, mask.device, torch.cuda.current_stream(mask.device).cuda_stream)
+        oc = self._order_caches.get(key)
+        if oc is None:
+            n = order_cache_ints(B, H, nqb, self.ORDER_CACHE_ENTRIES)
+            oc = torch.zeros(max(n, 1), dtype=torch.int32, device=mask.device)
+            self._order_caches[key] = oc
+        return oc
 
     def get(self, mask: torch.Tensor) -> BlockSparsePlan:
         key = id(mask)
@@ -107,7 +140,10 @@ class _PlanCache:
             ref, esig, plan = ent
             if ref() is mask and esig == sig:
                 return plan
-        plan = block_sparse_plan(mask)
+        if mask.dim() == 4 and mask.numel() > 0:
+            plan = block_sparse_plan(mask, self.order_cache(mask), self.ORDER_CACHE_ENTRIES)
+        else:
+            plan = block_sparse_plan(mask)
         entries = self._entries
         ref = weakref.ref(mask, lambda _r, k=key: entries.pop(k, None))
         entries[key] = (ref, sig, plan)
@@ -115,6 +151,7 @@ class _PlanCache:
 
     def clear(self) -> None:
         self._entries.clear()
+        self._order_caches.clear()
 
 
 PLAN_CACHE = _PlanCache()

@@ -203,6 +203,52 @@ def test_calibrator_block_64_head_dim_64():
     assert torch.allclose(mean, want, rtol=1e-5, atol=1e-8)
 
 
+@pytest.mark.slow
+def test_calibrator_full_wan_layers():
+    # BASELINE config 3 at full size: SinkMaskCalibrator.record on two Wan2.1-1.3B layers
+    # (B2 H12 N32760 d128 bf16, per-head sink keys at frame-0 positions) x two calls, then
+    # build_package (sparse_attention.py:537-608).  The package's masks must be the
+    # reference's coverage mask of the package's own means, bit for bit; the means must
+    # match the oracle's fp32 exact block mass (the mean over calls of the batch means) on
+    # sampled q-blocks, the ragged last one (120 rows) among them, within 1e-5 relative.
+    cfg = sa.SinkSparseConfig(pooling_mode="exact")
+    cal = sa.SinkMaskCalibrator(cfg)
+    B, H, N, D = 2, 12, 32760, 128
+    samples = [(0, 0), (3, 17), (7, 128), (11, 255), (5, 254)]   # (head, q-block)
+    rows_of = {}
+    for call in range(2):
+        for layer in range(2):
+            seed = 100 * layer + call
+            g = torch.Generator(device="cuda").manual_seed(seed)
+            q = torch.randn(B, H, N, D, device="cuda", dtype=torch.bfloat16, generator=g)
+            k = torch.randn(B, H, N, D, device="cuda", dtype=torch.bfloat16, generator=g)
+            gc = torch.Generator().manual_seed(seed)
+            for h in range(H):
+                k[:, h, torch.randint(0, 30 * 52, (4,), generator=gc).to("cuda")] *= 6.0
+            print(f"calibrator full size: layer {layer} call {call}", flush=True)
+            cal.record(layer, q, k, k)
+            for h, qb in samples:
+                r0, r1 = qb * 128, min((qb + 1) * 128, N)
+                rows_of[(layer, call, h, qb)] = (q[:, h:h + 1, r0:r1].cpu(), k[:, h:h + 1].cpu())
+            del q, k
+    pkg = cal.build_package(include_scores=True)
+    assert set(pkg["sink_masks"]) == {"0", "1"} and pkg["counts"] == {"0": 2, "1": 2}
+    for layer in range(2):
+        mean = pkg["mean_scores"][str(layer)]
+        assert mean.shape == (H, 256, 256) and mean.device.type == "cpu"
+        assert torch.equal(pkg["sink_masks"][str(layer)], torch_ref.coverage_mask(mean))
+        assert bool((pkg["std_scores"][str(layer)] >= 0).all())
+        for h, qb in samples:
+            per_call = []
+            for call in range(2):
+                qr, kr = rows_of[(layer, call, h, qb)]
+                per_call.append(torch_ref.exact_block_mass(qr, kr).mean(dim=0)[0, 0])   # batch mean
+            want = (per_call[0] + per_call[1]) / 2
+            got = mean[h, qb]
+            assert torch.allclose(got, want, rtol=1e-5, atol=1e-8), (layer, h, qb, (got - want).abs().max().item())
+            assert abs(float(got.double().sum()) - 1.0) < 1e-4
+
+
 def _serial_walk_rows(s, coverage):
     """Rows whose coverage cut lies past the range where fp64 prefix sums are exact in any
     order (the kernel scans that range across the wave and walks the rest serially):
