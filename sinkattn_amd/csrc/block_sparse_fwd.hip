@@ -167,8 +167,10 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_kernel(FwdArgs a) {
 // D = 128, bf16/f16: K and V tiles go global -> LDS by buffer DMA (no staging
 // registers; rows >= Nk read as zero through the buffer bounds), and V^T is read from
 // the row-major V tile with the gfx950 transpose read ds_read_b64_tr_b16.  K and V are
-// staged against each other: K(i+1) streams in while softmax(i) and PV(i) run, V(i+1)
-// while S(i+1) runs, with two work-group barriers per tile.  LDS layout: 128 rows x 16 chunks of 16 bytes per tile,
+// staged against each other: V(i)'s copies are spread over S(i), one per k-step, and
+// K(i+1)'s over softmax(i), one per step, so that the copies of the four waves never
+// queue up at the CU's vector-memory pipe in one burst; three work-group barriers per tile
+// (K free, V landed, V free and K(i+1) landed).  LDS layout: 128 rows x 16 chunks of 16 bytes per tile,
 // physical chunk = logical ^ (row & 15) for K and logical ^ (4 * (row & 3)) for V, which
 // keeps the 16-lane K reads and the 32-lane transpose reads on distinct banks.
 // ------------------------------------------------------------------------------------
@@ -208,36 +210,43 @@ __device__ __forceinline__ D128Lanes d128_lanes(int wave, int lane, uint32_t kst
   return L;
 }
 
+// Copy j (of 8) of this wave's share of a 128-row tile: rows 16j + 4w + lane/16, from the
+// buffer `rs` (rows past its size read as zero) into the LDS tile at `dst`.
+__device__ __forceinline__ void d128_copy_one(SA_LDS char* dst, const __amdgpu_buffer_rsrc_t& rs, uint32_t stride,
+                                              uint32_t lane_off, int wave, int j) {
+  dma16(rs, (SA_LDS void*)(dst + (256 * j + 64 * wave) * 16), lane_off + (uint32_t)j * 16u * stride);
+}
+
 // 128 rows of K (or V) from `base` (row stride `stride` bytes, `rows_valid` rows readable:
 // rows past it read as zero through the buffer bounds) into the LDS tile at `dst`.
 __device__ __forceinline__ void d128_copy_tile(SA_LDS char* dst, const char* base, uint32_t stride,
                                                int rows_valid, uint32_t lane_off, int wave) {
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)rows_valid * stride);
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    dma16(rs, (SA_LDS void*)(dst + (256 * j + 64 * wave) * 16), lane_off + (uint32_t)j * 16u * stride);
+  for (int j = 0; j < 8; ++j) d128_copy_one(dst, rs, stride, lane_off, wave, j);
 }
 
 // One 128-key tile of the d128 loop for this wave's 32 query rows:
-//   S^T = K Q^T from the K tile, barrier B1 (V has landed, every wave is done with K),
-//   after_b1() (the K buffer is free: the next K copy goes there), the online softmax,
-//   O^T += V^T P^T from the V tile, barrier B2 (the next K has landed, every wave is done
-//   with V), after_b2() (the V buffer is free).
+//   S^T = K Q^T from the K tile, with vcopy(j) (this tile's V copy j into the V buffer, free
+//   since the previous tile's B2) after the MFMAs of k-step j; barrier B1 (every wave is
+//   done with K); the online softmax with kcopy(j) (the next tile's K copy j into the K
+//   buffer) after step j; barrier BV (every wave's V copies have landed: vmcnt(8) leaves
+//   only the eight K copies issued after them in flight); O^T += V^T P^T from the V tile;
+//   barrier B2 (the next K has landed, every wave is done with V).  kcopy must issue a copy
+//   for every j, also after the last tile (then from a 0-byte buffer), so that the count
+//   of BV holds.
 // Keys at or past klim are masked; bias is added to the log2-domain logits (compensation
 // tiles); c = softmax scale * log2(e).
-template <int CT, typename FB1, typename FB2>
+template <int CT, typename FV, typename FK>
 __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, const D128Lanes& L,
                                           const u32x4 (&qf)[8], int key0, int klim, float bias,
                                           float c, int hl, f32x16 (&o)[4], float& m_run,
-                                          float& l_run, FB1&& after_b1, FB2&& after_b2) {
+                                          float& l_run, FV&& vcopy, FK&& kcopy) {
   constexpr int DS = 8, DT = 4;
   f32x16 s[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) s[t] = f32x16{};
   {
-    // Reads for k-step ds+1 are issued between the MFMAs of k-step ds, one read after
-    // each MFMA; the scheduling groups pin that order so no MFMA waits on the read
-    // issued just before it.
     u32x4 kr[2][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) kr[0][t] = *(SA_LDS const u32x4*)(lk + L.ka[0] + t * 8192);
@@ -252,11 +261,16 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
           kr[(ds + 1) & 1][t] = *(SA_LDS const u32x4*)(lk + L.ka[ds + 1] + t * 8192);
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
+        if (t == 1) {
+          vcopy(ds);  // V copy ds of this tile, one per k-step
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
       }
     }
   }
-  drain_then_barrier();  // B1
-  after_b1();
+  // B1: every wave is done reading K (own LDS reads returned); V copies may still fly
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0) only
+  __builtin_amdgcn_s_barrier();
 
   if (key0 + 128 > klim) {
 #pragma unroll
@@ -271,10 +285,6 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
 #pragma unroll
     for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
   mx = max_xor32(mx);
-  // Lazy rescale: the reference point m_run moves only when this tile's maximum exceeds
-  // it by more than kLazyRescaleLog2, so P = exp2(c*s + bias - m_run) stays at most 2^8
-  // (well inside the range of bf16/f16 P and fp32 O, l) and the 64 multiplies of O run
-  // on few tiles.  O / l and m_run + log2(l) do not depend on the reference point.
   const float m_tile = __builtin_fmaf(mx, c, bias);
   if (m_tile > m_run + kLazyRescaleLog2) {
     const float alpha = fast_exp2(m_run - m_tile);
@@ -283,10 +293,6 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
     for (int i = 0; i < DT; ++i) o[i] *= alpha;
     m_run = m_tile;
   }
-  // P in the MFMA's 16-bit type for PV; the row sum adds the fp32 values before that
-  // rounding (four independent partial sums), as the flash-attention forward does.  Plain
-  // fp32 adds, not v_dot2 of the packed pairs: the dot2 instructions stall while the other
-  // wave's MFMAs run on the SIMD (~11 cycles each, measured), plain VALU does not.
   u32x4 p[4][2];
   float lsum[4] = {0.f, 0.f, 0.f, 0.f};
   auto make_p = [&](int t, int u) {
@@ -298,7 +304,6 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
       lsum[t] += v0 + v1;
     }
   };
-  // V^T operand for d-tile dt of step (t, u): two transpose reads.
   auto vread = [&](int dt, int t, int u) -> u32x4 {
     const uint32_t off = t * 8192 + u * 4096;
     const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + L.va[dt][0] + off));
@@ -306,13 +311,17 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
     const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
     return u32x4{y0[0], y0[1], y1[0], y1[1]};
   };
-  // All of P first, then PV.  Each wave's tile then runs as three phases, S (MFMAs and K
-  // reads), softmax (VALU only) and PV (MFMAs and V^T transpose reads), and the VALU slots
-  // of S and PV stay free for the other work-group's wave on the SIMD, which is in another
-  // phase.  Interleaving the exps of later steps under the PV MFMAs (or the row max under S)
-  // measured slower.  Raised issue priority over PV.
+  // softmax, with the next tile's K copies spread over its steps
 #pragma unroll
-  for (int step = 0; step < 8; ++step) make_p(step >> 1, step & 1);
+  for (int step = 0; step < 8; ++step) {
+    make_p(step >> 1, step & 1);
+    kcopy(step);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // BV: this tile's V has landed for every wave (the own V copies are done once at most the
+  // eight K copies issued after them are in flight)
+  __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8) | (0 << 14));  // vmcnt(8)
+  __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_s_setprio(1);
   {
     u32x4 vr[2][DT];
@@ -327,7 +336,6 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) vr[(step + 1) & 1][dt] = vread(dt, nt, nu);
       }
-      // under each MFMA, two transpose reads of the next step
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         o[dt] = mfma32x32x16<CT>(vr[step & 1][dt], p[t][u], o[dt]);
@@ -338,8 +346,7 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
   }
   l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
   __builtin_amdgcn_s_setprio(0);
-  drain_then_barrier();  // B2
-  after_b2();
+  drain_then_barrier();  // B2: next K landed, every wave done with V
 }
 
 // Everything the d128 kernels need to know about one (b, h, q-block) work item.  All values
@@ -380,19 +387,13 @@ __device__ __forceinline__ int d128_key0(const D128Item& it, int t) {
   return t < it.cnt ? e * 128 : (t - it.cnt) * 128;
 }
 
-// K (or V) rows [key0, key0 + 128) of the listed keys (comp = false) or of the pooled keys
+// K rows [key0, key0 + 128) of the listed keys (comp = false) or of the pooled keys
 // (comp = true); rows at or past klim read as zero.
 template <int CT>
 __device__ __forceinline__ void d128_issue_k(const D128Item& it, int key0, int klim, bool comp, SA_LDS char* lk,
                                              const D128Lanes& L, uint32_t kstride, int wave) {
   const char* base = (comp ? it.kdbase : it.kbase) + (int64_t)key0 * kstride;
   d128_copy_tile(lk, base, kstride, klim - key0, L.k_off, wave);
-}
-template <int CT>
-__device__ __forceinline__ void d128_issue_v(const D128Item& it, int key0, int klim, bool comp, SA_LDS char* lv,
-                                             const D128Lanes& L, uint32_t vstride, int wave) {
-  const char* base = (comp ? it.vdbase : it.vbase) + (int64_t)key0 * vstride;
-  d128_copy_tile(lv, base, vstride, klim - key0, L.v_off, wave);
 }
 
 // O of this wave's 32 rows through its 8 KB of an idle LDS tile buffer: each lane holds
@@ -471,22 +472,23 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
   int klim = it.cnt > 0 ? Nk : Nd;
   if (it.ntot > 0) {
     d128_issue_k<CT>(it, key0, klim, it.cnt == 0, lk, L, kstride, wave);
-    d128_issue_v<CT>(it, key0, klim, it.cnt == 0, lv, L, vstride, wave);
-    // Drain both: waiting only for K(0) here leaves the compiler unable to prove at the
-    // loop head that V's copies do not alias the K reads, and it then waits there on
-    // every tile.
     drain_then_barrier();
   }
   for (int t = 0; t < it.ntot; ++t) {
     const bool next = t + 1 < it.ntot;
+    const bool comp = t >= it.cnt;
     const bool comp_next = t + 1 >= it.cnt;
-    // the next tile's first key: its list entry is loaded here, a whole S phase before the
-    // copies after B1 need it
     const int key0_next = d128_key0(it, t + 1);
     const int klim_next = comp_next ? Nd : Nk;
+    const __amdgpu_buffer_rsrc_t vrs =
+        make_rsrc((comp ? it.vdbase : it.vbase) + (int64_t)key0 * vstride, (uint32_t)(klim - key0) * vstride);
+    // after the last tile the K copies read nothing (a 0-byte buffer: zeros, no memory
+    // access), so that every tile issues the same copies and waits
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc((comp_next ? it.kdbase : it.kbase) + (int64_t)key0_next * kstride,
+                                                 next ? (uint32_t)(klim_next - key0_next) * kstride : 0u);
     d128_tile<CT>(lk, lv, L, qf, key0, klim, t < it.cnt ? 0.f : comp_bias, c, hl, o, m_run, l_run,
-                  [&] { if (next) d128_issue_k<CT>(it, key0_next, klim_next, comp_next, lk, L, kstride, wave); },
-                  [&] { if (next) d128_issue_v<CT>(it, key0_next, klim_next, comp_next, lv, L, vstride, wave); });
+                  [&](int j) { d128_copy_one(lv, vrs, vstride, L.v_off, wave, j); },
+                  [&](int j) { d128_copy_one(lk, krs, kstride, L.k_off, wave, j); });
     key0 = key0_next;
     klim = klim_next;
   }
