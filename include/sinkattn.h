@@ -207,14 +207,16 @@ int sinkattn_lse_mix(const void* sink_out, const int64_t sink_strides[4],
  *     P = softmax_rows(scale * Q K^T)                  (fp32, over all Nk keys)
  *     out[b,h,qb,kb] = mean over the rows r of q-block qb of  sum_{j in kb} P[r,j]
  * out is fp32 [B,H,nqb,nkb] contiguous, nqb = ceil(Nq/block), nkb = ceil(Nk/block).
- * block_size 128 with D 128: bf16/f16 inputs use the bf16/f16 matrix cores (products are
- * exact, sums fp32) and a device workspace of sinkattn_block_mass_pool_workspace_bytes()
- * bytes (per-row block sums of the resident work-groups, queried for the current
- * device); f32 inputs use the fp32 matrix cores (nkb <= 256) and need no workspace.
- * Every other shape (block_size 1..1024, D 1..256, f32 with nkb > 256) runs a generic
- * kernel (fp32 dot products, two passes over the keys, no workspace; the query may still
- * return a size for block_size 128, which the call then leaves unused), limited by LDS to
- * about (160 KiB / 4 - 128 (D + 1) - 4160) key blocks.
+ * block_size 16, 32, 64 or 128 with D 128: bf16/f16 inputs use the bf16/f16 matrix cores
+ * (products are exact, sums fp32) and a device workspace of
+ * sinkattn_block_mass_pool_workspace_bytes() bytes (per-row block sums of the resident
+ * work-groups, queried for the current device); f32 inputs at block_size 128, D 128 use
+ * the fp32 matrix cores (nkb <= 256) and need no workspace.  Every other shape
+ * (block_size 1..1024, D 1..256, f32 otherwise) runs a generic kernel (fp32 dot products,
+ * two passes over the keys, no workspace; the query may still return a size for a
+ * matrix-core block size, which the call then leaves unused), limited by LDS to about
+ * (160 KiB / 4 - 128 (D + 1) - 4160) key blocks.  Callers with a 16-bit head dim below 128
+ * may zero-pad it to 128 to take the matrix cores (zeros leave every dot product exact).
  * ---------------------------------------------------------------------------------- */
 size_t sinkattn_block_mass_pool_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nk,
                                                 int64_t block_size, int dtype);

@@ -412,10 +412,15 @@ static int check_generic_pool(const char* who, const sa::PoolArgs& a, int dtype)
   return 0;
 }
 
+// Block sizes the persistent matrix-core block-mass kernel takes (head dim 128, 16-bit).
+static bool mass_mfma_block(int64_t block_size) {
+  return block_size == 16 || block_size == 32 || block_size == 64 || block_size == 128;
+}
+
 size_t sinkattn_block_mass_pool_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nk,
                                                 int64_t block_size, int dtype) {
-  if (dtype == SINKATTN_F32 || block_size <= 0) return 0;
-  const int64_t items = B * H * cdiv(Nq, block_size);
+  if (dtype == SINKATTN_F32 || !mass_mfma_block(block_size)) return 0;
+  const int64_t items = B * H * cdiv(Nq, 128);  // items of 128 query rows
   const int64_t groups = items < sa::block_mass_groups() ? items : sa::block_mass_groups();
   return (size_t)(groups * cdiv(Nk, block_size) * 128 * (int64_t)sizeof(float));
 }
@@ -434,7 +439,7 @@ int sinkattn_block_mass_pool(const void* q, const void* k, int dtype, int64_t B,
   a.out = out;
   a.ws = reinterpret_cast<float*>(workspace);
   const bool at128 = block_size == 128 && D == 128;
-  if (at128 && dtype != SINKATTN_F32) {  // persistent MFMA kernel, workspace slots
+  if (mass_mfma_block(block_size) && D == 128 && dtype != SINKATTN_F32) {  // persistent MFMA kernel, workspace slots
     if (workspace == nullptr) return fail("block_mass_pool: null workspace");
     if (k_strides[2] < D) return fail("block_mass_pool: k row stride below the head dim");
     if (Nk * k_strides[2] * 2 >= (int64_t)1 << 31)

@@ -31,27 +31,40 @@ namespace sa {
 constexpr float kRescaleMargin = 8.f;  // block_mass_f32_kernel only
 
 // ------------------------------------------------------------------------------------
-// Exact block mass, 16-bit inputs, persistent work-groups (up to 3 per CU).
-// Each work-group walks (b, h, q-block) items; per item it streams every K tile into
-// LDS by buffer DMA (rows >= Nk read as zero and are masked), computes S^T for its 128
-// rows with the matrix cores and writes each row's per-key-block sum of
-// exp2(scale*log2e*s - m_ref) to its private workspace slot ws[kb][row].  m_ref is the
-// row maximum of the first tile; it only moves (and the row's earlier sums are
-// rescaled) if a tile's sum overflows 2^64, i.e. when scores rise more than ~64 log2
-// units above it.  The item's epilogue normalises every row by its total and averages
-// the rows of each key block.
+// Exact block mass, 16-bit inputs, head dim 128, block size KB in {16, 32, 64, 128};
+// persistent work-groups (up to 3 per CU).
+// Each work-group walks items of 128 query rows (128 / KB q-blocks of the map); per item it
+// streams every 128-key K tile into LDS by buffer DMA (rows >= Nk read as zero and are
+// masked), computes S^T for its 128 rows with the matrix cores and writes each row's sum
+// of exp2(scale*log2e*s - m_ref) over every KB-key block of the tile to its private
+// workspace slot ws[kb][row] (kb in KB units).  m_ref is the row maximum of the first tile;
+// it only moves (and the row's earlier sums are rescaled) if a tile's sum overflows 2^64,
+// i.e. when scores rise more than ~64 log2 units above it.  The item's epilogue normalises
+// every row by its total and averages the rows of each q-block per key block.
+// Key of register j of a lane of 32-key group t, within the group: tile_key(hl, j) =
+// (j & 3) + 4 ((j >> 2) & 1) + 8 hl + 16 (j >> 3), so the KB-key block of (t, j) does not
+// depend on the lane: t / (KB / 32) for KB >= 32, 2 t + (j >> 3) for KB = 16 (the lane pair
+// holds its two 8-key halves).
 // ------------------------------------------------------------------------------------
 constexpr float kSumLimit = 1.8446744073709552e19f;  // 2^64
 
-template <int CT>
+template <int KB>
+__device__ __forceinline__ constexpr int sub_block(int t, int j) {
+  return KB == 16 ? 2 * t + (j >> 3) : (t * 32) / KB;
+}
+
+template <int CT, int KB>
 __global__ __launch_bounds__(256, 3) void block_mass_persistent_kernel(PoolArgs a, int items) {
   constexpr int DS = 8;
+  constexpr int NS = 128 / KB;  // key blocks per 128-key tile, q-blocks per 128-row item
   __shared__ u32x4 lds_k[2048];
   __shared__ float row_inv[128];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, l32 = lane & 31;
-  const int nkb = a.nkb;
+  const int nkb = a.nkb;                 // key blocks of the map (KB keys each)
+  const int ntiles = (a.Nk + 127) >> 7;  // 128-key tiles
+  const int nqi = (a.Nq + 127) >> 7;     // 128-row items per head
   float* ws = a.ws + (size_t)blockIdx.x * (size_t)nkb * 128;
   const uint32_t kstride = (uint32_t)a.ks[2] * 2;
   const int drow = 4 * wave + (lane >> 4);
@@ -65,19 +78,19 @@ __global__ __launch_bounds__(256, 3) void block_mass_persistent_kernel(PoolArgs 
   const int r = wave * 32 + l32;
 
   for (int item = blockIdx.x; item < items; item += gridDim.x) {
-    const int bh = item / a.nqb;
-    const int qb = item - bh * a.nqb;
+    const int bh = item / nqi;
+    const int qi = item - bh * nqi;
     const int b = bh / a.H, h = bh - b * a.H;
     const char* qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * 2;
     const char* kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)h * a.ks[1]) * 2;
-    const int qrow = qb * 128 + r;
+    const int qrow = qi * 128 + r;
     u32x4 qf[DS];
     load_q_operand<CT, CT, 128>(qf, qbase, a.qs[2], qrow, a.Nq, hl);
     float m_ref = neg_inf();
     float l_tot = 0.f;
 
-    for (int kb = 0; kb < nkb; ++kb) {
-      const int key0 = kb * 128;
+    for (int kt = 0; kt < ntiles; ++kt) {
+      const int key0 = kt * 128;
       __syncthreads();  // the previous tile (or item epilogue) is done with lds_k
       {
         const __amdgpu_buffer_rsrc_t rs =
@@ -104,7 +117,7 @@ __global__ __launch_bounds__(256, 3) void block_mass_persistent_kernel(PoolArgs 
           for (int j = 0; j < 16; ++j)
             if (key0 + t * 32 + tile_key(hl, j) >= a.Nk) s[t][j] = neg_inf();
       }
-      if (kb == 0) {  // reference maximum from the first tile (key 0 always exists)
+      if (kt == 0) {  // reference maximum from the first tile (key 0 always exists)
         float mx = neg_inf();
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -112,13 +125,22 @@ __global__ __launch_bounds__(256, 3) void block_mass_persistent_kernel(PoolArgs 
           for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
         m_ref = max_xor32(mx) * c;
       }
-      float ps = 0.f;
+      float ps[NS];
+      auto sums = [&]() {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+        for (int i = 0; i < NS; ++i) ps[i] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) ps += fast_exp2(__builtin_fmaf(s[t][j], c, -m_ref));
-      ps = sum_xor32(ps);
-      if (!(ps <= kSumLimit)) {
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) ps[sub_block<KB>(t, j)] += fast_exp2(__builtin_fmaf(s[t][j], c, -m_ref));
+#pragma unroll
+        for (int i = 0; i < NS; ++i) ps[i] = sum_xor32(ps[i]);
+      };
+      sums();
+      float tot = 0.f;
+#pragma unroll
+      for (int i = 0; i < NS; ++i) tot += ps[i];
+      if (!(tot <= kSumLimit)) {
         // Rare: scores far above m_ref.  Move m_ref to this tile's maximum and rescale
         // the row's earlier sums (the two lanes of the row split them by parity).
         float mx = neg_inf();
@@ -128,36 +150,56 @@ __global__ __launch_bounds__(256, 3) void block_mass_persistent_kernel(PoolArgs 
           for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
         mx = max_xor32(mx) * c;
         const float f = fast_exp2(m_ref - mx);
-        for (int j = hl; j < kb; j += 2) ws[j * 128 + r] *= f;
+        for (int j = hl; j < kt * NS; j += 2) ws[j * 128 + r] *= f;
         l_tot *= f;
         m_ref = mx;
-        ps = 0.f;
+        sums();
+        tot = 0.f;
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) ps += fast_exp2(__builtin_fmaf(s[t][j], c, -m_ref));
-        ps = sum_xor32(ps);
+        for (int i = 0; i < NS; ++i) tot += ps[i];
       }
-      l_tot += ps;
-      if (hl == 0) ws[kb * 128 + r] = ps;
+      l_tot += tot;
+      // the lanes of a row split the stores: lane half hl stores key blocks i = hl (mod 2)
+#pragma unroll
+      for (int i = 0; i < NS; ++i)
+        if ((NS == 1 ? hl == 0 : (i & 1) == hl) && kt * NS + i < nkb) ws[(kt * NS + i) * 128 + r] = ps[i];
     }
 
-    // Epilogue: out[kb] = mean over the block's rows of ws[kb][row] / total(row).
-    const int nrows = min(128, a.Nq - qb * 128);
-    if (hl == 0) row_inv[r] = (r < nrows) ? 1.f / fmaxf(l_tot, 1e-6f) : 0.f;
+    // Epilogue: out[qb][kb] = mean over the q-block's rows of ws[kb][row] / total(row); lane l
+    // holds rows l and l + 64, so a q-block of KB rows is one group of KB lanes (KB < 64) or
+    // a whole half (KB = 64) or both halves (KB = 128).
+    if (hl == 0) row_inv[r] = (qrow < a.Nq) ? 1.f / fmaxf(l_tot, 1e-6f) : 0.f;
     __syncthreads();
     const float inv0 = row_inv[lane], inv1 = row_inv[lane + 64];
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(ws, (uint32_t)nkb * 512u);
-    float* out = reinterpret_cast<float*>(a.out) + ((int64_t)bh * a.nqb + qb) * nkb;
-    const float inv_n = 1.f / (float)nrows;
+    float* out = reinterpret_cast<float*>(a.out);
     for (int kb = wave; kb < nkb; kb += 4) {
       // coherent (L1-bypassing) loads of values other waves of the group wrote
       const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4), 0, 1));
       const float x1 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4 + 256), 0, 1));
-      float v = x0 * inv0 + x1 * inv1;
+      float v0 = x0 * inv0, v1 = x1 * inv1;
+      if constexpr (KB == 128) {
+        v0 += v1;
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-      if (lane == 0) out[kb] = v * inv_n;
+        for (int off = 32; off >= 1; off >>= 1) v0 += __shfl_xor(v0, off, 64);
+      } else {
+#pragma unroll
+        for (int off = (KB >= 64 ? 32 : KB / 2); off >= 1; off >>= 1) {
+          v0 += __shfl_xor(v0, off, 64);
+          v1 += __shfl_xor(v1, off, 64);
+        }
+      }
+      if (lane % (KB >= 64 ? 64 : KB) == 0) {
+        const int g = lane / (KB >= 64 ? 64 : KB);  // q-block of the first half
+#pragma unroll
+        for (int half = 0; half < (KB == 128 ? 1 : 2); ++half) {
+          const int qs = half * (NS / 2 > 0 ? NS / 2 : 1) + g;  // q-block within the item
+          const int qb = qi * NS + qs;
+          const int rows = min(KB, a.Nq - qb * KB);
+          if (qb < a.nqb && rows > 0)
+            out[((int64_t)bh * a.nqb + qb) * nkb + kb] = (half == 0 ? v0 : v1) / (float)rows;
+        }
+      }
     }
   }
 }
@@ -492,12 +534,22 @@ hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream
     else block_mass_f32_kernel<256><<<grid, 256, 0, stream>>>(a);
     return hipGetLastError();
   }
-  const int items = a.B * a.H * a.nqb;
+  const int items = a.B * a.H * ((a.Nq + 127) / 128);
   const int groups = min(items, block_mass_groups());
-  if (dtype == kBF16)
-    block_mass_persistent_kernel<kBF16><<<groups, 256, 0, stream>>>(a, items);
-  else
-    block_mass_persistent_kernel<kF16><<<groups, 256, 0, stream>>>(a, items);
+#define SA_MASS(KB)                                                                     \
+  do {                                                                                  \
+    if (dtype == kBF16)                                                                 \
+      block_mass_persistent_kernel<kBF16, KB><<<groups, 256, 0, stream>>>(a, items);    \
+    else                                                                                \
+      block_mass_persistent_kernel<kF16, KB><<<groups, 256, 0, stream>>>(a, items);     \
+  } while (0)
+  switch (a.bs) {
+    case 16: SA_MASS(16); break;
+    case 32: SA_MASS(32); break;
+    case 64: SA_MASS(64); break;
+    default: SA_MASS(128); break;
+  }
+#undef SA_MASS
   return hipGetLastError();
 }
 

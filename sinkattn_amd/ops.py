@@ -40,15 +40,22 @@ def _kernel_operand(t: torch.Tensor) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
-def _pad_head_dim(t: torch.Tensor) -> torch.Tensor:
-    """Zero-pad the head dim of a pooling operand to a multiple of 16 (16-bit dtypes: the
-    matrix-core score path) or 8 (fp32: the 8-element stride rule); dot products, the only
-    use of the head dim in the pooling modes, are unchanged by zero padding."""
+def _pad_head_dim(t: torch.Tensor, to: Optional[int] = None) -> torch.Tensor:
+    """Zero-pad the head dim of a pooling operand to `to`, or else to a multiple of 16
+    (16-bit dtypes: the matrix-core score path) or 8 (fp32: the 8-element stride rule); dot
+    products, the only use of the head dim in the pooling modes, are unchanged by zero
+    padding."""
     D = int(t.shape[-1])
+    if to is not None and D < to:
+        return torch.nn.functional.pad(t, (0, to - D))
     mult = 8 if t.dtype == torch.float32 else 16
     if D % mult == 0:
         return t
     return torch.nn.functional.pad(t, (0, mult - D % mult))
+
+
+# Block sizes of the matrix-core exact block-mass kernel (16-bit inputs, head dim 128).
+MASS_MFMA_BLOCKS = (16, 32, 64, 128)
 
 
 @dataclass
@@ -390,7 +397,9 @@ def block_mass_scores(q: torch.Tensor, k: torch.Tensor, block_size: int = 128,
     dt = _lib.dtype_code(q.dtype)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    qk, kk = _kernel_operand(_pad_head_dim(q)), _kernel_operand(_pad_head_dim(k))
+    # a 16-bit head dim below 128 is zero-padded to 128 for the matrix-core kernel
+    to = 128 if (q.dtype != torch.float32 and D < 128 and int(block_size) in MASS_MFMA_BLOCKS) else None
+    qk, kk = _kernel_operand(_pad_head_dim(q, to)), _kernel_operand(_pad_head_dim(k, to))
     D = int(qk.shape[-1])
     out = torch.empty((B, H, _cdiv(Nq, block_size), _cdiv(Nk, block_size)), dtype=torch.float32,
                       device=q.device)

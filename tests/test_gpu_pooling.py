@@ -81,6 +81,40 @@ def test_exact_mass_rescale_path_sinks_last():
         _close(ops.block_mass_scores(qq.cuda(), kk.cuda()), torch_ref.exact_block_mass(qq, kk))
 
 
+# The matrix-core exact block-mass kernel at block sizes 16, 32 and 64 (16-bit inputs, head
+# dim 128; smaller head dims are zero-padded to 128): q-blocks of KB rows inside 128-row
+# items, key blocks of KB keys inside 128-key tiles, ragged ends on both sides, Nq != Nk.
+@pytest.mark.parametrize("bs", [16, 32, 64])
+@pytest.mark.parametrize("D,Nq,Nk,dtype", [(128, 1000, 1000, torch.bfloat16), (128, 333, 1111, torch.float16),
+                                           (64, 520, 260, torch.bfloat16)])
+def test_exact_mass_mfma_block_sizes(bs, D, Nq, Nk, dtype):
+    q, k = _qkd(2, 3, 3, Nq, Nk, D, dtype, seed=bs + Nq, sinks=3)
+    ours = ops.block_mass_scores(q.cuda(), k.cuda(), block_size=bs)
+    ref = torch_ref.exact_block_mass(q, k, block_size=bs)
+    assert ours.shape == ref.shape == (2, 3, math.ceil(Nq / bs), math.ceil(Nk / bs))
+    _close(ours, ref)
+    assert torch.allclose(ours.cpu().sum(-1), torch.ones(ref.shape[:-1]), atol=1e-5)
+
+
+@pytest.mark.parametrize("bs", [16, 32, 64, 128])
+def test_exact_mass_mfma_rescale_and_persistent_loop(bs):
+    # 96 heads x 9 items of 128 rows: more items than resident work-groups, so slots are
+    # reused.  q = 0.5 + 0.1 N(0,1) and the first 128 keys all -10: those scores are about
+    # -640, ~80 log2 units below the N(0,1) keys after them, so the first tile's maximum
+    # (the rows' reference point) sends every row through the 2^64 rescale of its earlier
+    # key-block sums on the second tile (moderate scores elsewhere keep fp32 summation-order
+    # differences below the 1e-5 bar)
+    g = torch.Generator().manual_seed(bs)
+    q = 0.5 + 0.1 * torch.randn(1, 96, 1100, 128, generator=g)
+    k = torch.randn(1, 96, 1500, 128, generator=g)
+    k[:, :, :128] = -10.0
+    qq, kk = q.bfloat16(), k.bfloat16()
+    ours = ops.block_mass_scores(qq.cuda(), kk.cuda(), block_size=bs)
+    ref = torch_ref.exact_block_mass(qq, kk, block_size=bs)
+    _close(ours, ref)
+    assert float(ours[..., : 128 // bs].sum(-1).max()) < 1e-20   # the first tile holds no mass
+
+
 def test_exact_mass_closed_forms():
     # Q = 0: uniform softmax -> mass = |kb| / N (last block 120 of 32760 -> 120/N)
     N = 1016  # 7 full blocks + 120
