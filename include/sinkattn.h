@@ -235,12 +235,12 @@ int sinkattn_block_mass_pool(const void* q, const void* k, int dtype,
  *     m_r      = max over kb of the unrounded block maxima
  *     Po[qb,kb]= q.dtype( max_{r in qb} exp2(R[r,kb] - m_r) )
  *     Po      /= q.dtype( sum_kb Po[qb,kb] )           (row normalisation in q.dtype)
- Po is written in q.dtype (bf16, f16 or f32) as [B,H,nd,nd] contiguous.  kv head of query
+ * Po is written in q.dtype (bf16, f16 or f32) as [B,H,nd,nd] contiguous.  kv head of query
  * head h is h / (H / Hk).  causal restricts row qb to kb <= qb and adds -1e6 to the
  * raw scores above the diagonal of the diagonal tile, as the reference does.  Keys and
  * rows >= N are excluded (the reference leaves ragged N undefined).  block_size in
  * {16, 32, 64, 128}, D in {16, 32, 64, 128, 256} (the reference's asserts).  bf16/f16 with
- * block_size 128, D 128 and nd <= 1024 run the persistent MFMA kernel: `workspace` is a
+ * D 128 (nd <= 1024 at block_size 128) run the persistent MFMA kernel: `workspace` is a
  * device buffer of at least sinkattn_max_pool_workspace_bytes(...) bytes (per-(row,
  * key-block) maxima of the rows in flight); calls that share one workspace must be
  * ordered on one stream.  Other shapes run the generic kernel (no workspace; same LDS

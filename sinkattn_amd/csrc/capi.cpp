@@ -453,10 +453,12 @@ int sinkattn_block_mass_pool(const void* q, const void* k, int dtype, int64_t B,
 }
 
 size_t sinkattn_max_pool_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t block_size, int dtype) {
-  if (dtype == SINKATTN_F32 || block_size <= 0) return 0;
-  const int64_t items = B * H * cdiv(N, block_size);
+  if (dtype == SINKATTN_F32 || !mass_mfma_block(block_size)) return 0;
+  const int64_t items = B * H * cdiv(N, 128);  // items of 128 query rows
   const int64_t groups = items < sa::max_pool_groups() ? items : sa::max_pool_groups();
-  return (size_t)(groups * cdiv(N, block_size) * 128 * (int64_t)sizeof(float));
+  // per group: the rows' block maxima, and below block 128 the item's column maxima
+  const int64_t per_kb = 128 + (block_size == 128 ? 0 : 128 / block_size);
+  return (size_t)(groups * cdiv(N, block_size) * per_kb * (int64_t)sizeof(float));
 }
 
 int sinkattn_max_pool(const void* q, const void* k, int dtype, int64_t B, int64_t H, int64_t Hk,
@@ -478,7 +480,7 @@ int sinkattn_max_pool(const void* q, const void* k, int dtype, int64_t B, int64_
   a.causal = causal ? 1 : 0;
   a.out = po;
   a.ws = static_cast<float*>(workspace);
-  if (dtype != SINKATTN_F32 && block_size == 128 && D == 128 && a.nkb <= 1024) {
+  if (dtype != SINKATTN_F32 && D == 128 && (block_size != 128 || a.nkb <= 1024)) {
     // persistent MFMA kernel, workspace slots
     if (workspace == nullptr) return fail("max_pool: null workspace (see sinkattn_max_pool_workspace_bytes)");
     if (k_strides[2] < D || N * k_strides[2] * 2 >= (int64_t)1 << 31)

@@ -318,29 +318,36 @@ __device__ __forceinline__ float round_to<kF16>(float x) {
 }
 
 // ------------------------------------------------------------------------------------
-// Max-pool map, persistent form (bf16/f16): the structure of block_mass_persistent_kernel
-// (K tiles by DMA, S^T on the matrix cores) with the block maxima of each row kept in the
-// group's workspace slot ws[kb][row] instead of LDS, so four groups (37 KB of LDS, 128
-// VGPRs each) fit a CU: per tile a group waits for its own copy, and the other three
-// cover that wait.  Per tile: R[r,kb] = q.dtype(max_j s * sm_scale * log2e) (raw-score maximum first,
-// then the scale, as pooling_kernel.py:39-48 does), m_r = max over kb of the unrounded
-// values.  Epilogue per kb: Po[kb] = q.dtype(max over the block's rows of
-// exp2(R[r,kb] - m_r)), then the row is normalised in q.dtype (pooling_kernel.py:65-75,
-// 243-244).  kv head = h / (H / Hk); causal restricts kb <= qb and adds -1e6 above the
-// diagonal of the diagonal tile.
+// Max-pool map, persistent form (bf16/f16, head dim 128, block size KB in {16, 32, 64,
+// 128}): the structure of block_mass_persistent_kernel (items of 128 query rows, K tiles of
+// 128 keys by DMA, S^T on the matrix cores) with the block maxima of each row kept in the
+// group's workspace slot ws[kb][row] instead of LDS, so four groups (33-37 KB of LDS, 128
+// VGPRs each) fit a CU: per tile a group waits for its own copy, and the other three cover
+// that wait.  Per tile: R[r,kb] = q.dtype(max_j s * sm_scale * log2e) for each KB-key block
+// (raw-score maximum first, then the scale, as pooling_kernel.py:39-48 does), m_r = max
+// over kb of the unrounded values.  Epilogue per q-block and kb: Po[kb] = q.dtype(max over
+// the block's rows of exp2(R[r,kb] - m_r)), then the row is normalised in q.dtype
+// (pooling_kernel.py:65-75, 243-244).  kv head = h / (H / Hk); causal restricts kb <= qb and
+// adds -1e6 to the raw scores above the diagonal of the diagonal block.  Block 128 keeps
+// the item's column maxima in LDS (nkb <= 1024); smaller blocks keep them after the
+// group's slot, in (128 / KB) * nkb floats of the workspace.
 // ------------------------------------------------------------------------------------
-template <int CT>
+template <int CT, int KB>
 __global__ __launch_bounds__(256, 4) void max_pool_persistent_kernel(PoolArgs a, int items) {
   constexpr int DS = 8;
+  constexpr int NS = 128 / KB;  // key blocks per tile, q-blocks per item
   __shared__ u32x4 lds_k[2048];
   __shared__ float row_m[128];
-  __shared__ float colmax[1024];
-  __shared__ float total_sh;
+  __shared__ float colmax[KB == 128 ? 1024 : 1];
+  __shared__ float total_sh[KB == 128 ? 1 : 4];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, l32 = lane & 31;
   const int nkb = a.nkb;
-  float* ws = a.ws + (size_t)blockIdx.x * (size_t)nkb * 128;
+  const int ntiles = (a.Nk + 127) >> 7;
+  const int nqi = (a.Nq + 127) >> 7;
+  float* ws = a.ws + (size_t)blockIdx.x * (size_t)nkb * (128 + (KB == 128 ? 0 : NS));
+  float* cm = ws + (size_t)nkb * 128;  // [NS][nkb] column maxima (KB < 128)
   const uint32_t kstride = (uint32_t)a.ks[2] * 2;
   const int drow = 4 * wave + (lane >> 4);
   const uint32_t k_off = (uint32_t)drow * kstride + (uint32_t)(((lane & 15) ^ (drow & 15)) * 16);
@@ -353,20 +360,22 @@ __global__ __launch_bounds__(256, 4) void max_pool_persistent_kernel(PoolArgs a,
   const int r = wave * 32 + l32;
 
   for (int item = blockIdx.x; item < items; item += gridDim.x) {
-    const int bh = item / a.nqb;
-    const int qb = item - bh * a.nqb;
+    const int bh = item / nqi;
+    const int qi = item - bh * nqi;
     const int b = bh / a.H, h = bh - b * a.H;
     const int hk = h / (a.H / a.Hk);
-    const int kb_end = a.causal ? min(nkb, qb + 1) : nkb;
+    const int kt_end = a.causal ? min(ntiles, qi + 1) : ntiles;
+    const int kb_item = a.causal ? min(nkb, (qi + 1) * NS) : nkb;  // key blocks any row of the item sees
     const char* qbase = (const char*)a.q + ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[1]) * 2;
     const char* kbase = (const char*)a.k + ((int64_t)b * a.ks[0] + (int64_t)hk * a.ks[1]) * 2;
-    const int qrow = qb * 128 + r;
+    const int qrow = qi * 128 + r;
+    const int qbr = qrow / KB;  // this row's q-block
     u32x4 qf[DS];
     load_q_operand<CT, CT, 128>(qf, qbase, a.qs[2], qrow, a.Nq, hl);
     float m = neg_inf();
 
-    for (int kb = 0; kb < kb_end; ++kb) {
-      const int key0 = kb * 128;
+    for (int kt = 0; kt < kt_end; ++kt) {
+      const int key0 = kt * 128;
       __syncthreads();  // the previous tile (or item epilogue) is done with lds_k
       {
         const __amdgpu_buffer_rsrc_t rs =
@@ -400,57 +409,108 @@ __global__ __launch_bounds__(256, 4) void max_pool_persistent_kernel(PoolArgs a,
           }
         }
       }
-      const bool diag = a.causal && kb == qb;
+      const bool diag = a.causal && kt == qi;
       if (key0 + 128 > a.Nk || diag) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             const int key = key0 + t * 32 + tile_key(hl, j);
-            if (diag && qrow < key) s[t][j] += -1.0e6f;
+            if (diag) {
+              const int kbk = key / KB;
+              if (kbk == qbr && qrow < key) s[t][j] += -1.0e6f;
+              if (kbk > qbr) s[t][j] = neg_inf();  // a key block past the row's own: not seen
+            }
             if (key >= a.Nk) s[t][j] = neg_inf();
           }
       }
-      float mx = neg_inf();
+      float mx[NS];
+#pragma unroll
+      for (int i = 0; i < NS; ++i) mx[i] = neg_inf();
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
-      mx = max_xor32(mx) * qk_scale;
-      m = fmaxf(m, mx);
-      if (hl == 0) ws[kb * 128 + r] = round_to<CT>(mx);
+        for (int j = 0; j < 16; ++j) mx[sub_block<KB>(t, j)] = fmaxf(mx[sub_block<KB>(t, j)], s[t][j]);
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        mx[i] = max_xor32(mx[i]) * qk_scale;
+        m = fmaxf(m, mx[i]);
+        if ((NS == 1 ? hl == 0 : (i & 1) == hl) && kt * NS + i < nkb) ws[(kt * NS + i) * 128 + r] = round_to<CT>(mx[i]);
+      }
     }
 
     // Epilogue.  Rows past the end of the sequence take no part (m = +inf gives 0).
-    const int nrows = min(128, a.Nq - qb * 128);
-    if (hl == 0) row_m[r] = (r < nrows) ? m : pos_inf();
+    if (hl == 0) row_m[r] = (qrow < a.Nq) ? m : pos_inf();
     __syncthreads();
     const float m0 = row_m[lane], m1 = row_m[lane + 64];
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(ws, (uint32_t)nkb * 512u);
-    for (int kb = wave; kb < kb_end; kb += 4) {
-      // coherent (L1-bypassing) loads of values other waves of the group wrote
-      const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4), 0, 1));
-      const float x1 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4 + 256), 0, 1));
-      float v = fmaxf(fast_exp2(x0 - m0), fast_exp2(x1 - m1));
+    if constexpr (KB == 128) {
+      for (int kb = wave; kb < kb_item; kb += 4) {
+        // coherent (L1-bypassing) loads of values other waves of the group wrote
+        const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4), 0, 1));
+        const float x1 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4 + 256), 0, 1));
+        float v = fmaxf(fast_exp2(x0 - m0), fast_exp2(x1 - m1));
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-      if (lane == 0) colmax[kb] = round_to<CT>(v);
-    }
-    __syncthreads();
-    // Row normalisation in q.dtype: sum (fp32 accumulate, rounded), then divide.
-    if (wave == 0) {
-      float part = 0.f;
-      for (int kb = lane; kb < kb_end; kb += 64) part += colmax[kb];
+        for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+        if (lane == 0) colmax[kb] = round_to<CT>(v);
+      }
+      __syncthreads();
+      // Row normalisation in q.dtype: sum (fp32 accumulate, rounded), then divide.
+      if (wave == 0) {
+        float part = 0.f;
+        for (int kb = lane; kb < kb_item; kb += 64) part += colmax[kb];
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
-      if (lane == 0) total_sh = round_to<CT>(part);
-    }
-    __syncthreads();
-    const float total = total_sh;
-    uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * a.nqb + qb) * nkb;
-    for (int kb = tid; kb < nkb; kb += 256) {
-      const float v = kb < kb_end ? colmax[kb] / total : 0.f;
-      out[kb] = (uint16_t)(pack2<CT>(v, 0.f) & 0xffffu);
+        for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+        if (lane == 0) total_sh[0] = round_to<CT>(part);
+      }
+      __syncthreads();
+      const float total = total_sh[0];
+      uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * a.nqb + qi) * nkb;
+      for (int kb = tid; kb < nkb; kb += 256) {
+        const float v = kb < kb_item ? colmax[kb] / total : 0.f;
+        out[kb] = (uint16_t)(pack2<CT>(v, 0.f) & 0xffffu);
+      }
+    } else {
+      // Pass 1: column maxima of every (q-block, key block) of the item into cm[qs][kb]:
+      // lane l holds rows l and l + 64, so a q-block is a group of KB lanes (KB < 64) or a
+      // whole half (KB = 64).
+      constexpr int G = KB >= 64 ? 64 : KB;
+      for (int kb = wave; kb < kb_item; kb += 4) {
+        const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4), 0, 1));
+        const float x1 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (uint32_t)(kb * 512 + lane * 4 + 256), 0, 1));
+        float v0 = fast_exp2(x0 - m0), v1 = fast_exp2(x1 - m1);
+#pragma unroll
+        for (int off = G / 2; off >= 1; off >>= 1) {
+          v0 = fmaxf(v0, __shfl_xor(v0, off, 64));
+          v1 = fmaxf(v1, __shfl_xor(v1, off, 64));
+        }
+        if (lane % G == 0) {
+          const int g = lane / G;
+          cm[(size_t)g * nkb + kb] = round_to<CT>(v0);
+          cm[(size_t)(NS / 2 + g) * nkb + kb] = round_to<CT>(v1);
+        }
+      }
+      __syncthreads();  // the column maxima are in memory (the barrier drains this group's stores)
+      // Pass 2: per q-block (one wave each), the row total in q.dtype, then the division.
+      const __amdgpu_buffer_rsrc_t crs = make_rsrc(cm, (uint32_t)(NS * nkb) * 4u);
+      for (int qs = wave; qs < NS; qs += 4) {
+        const int qb = qi * NS + qs;
+        if (qb >= a.nqb) continue;
+        const int kb_end = a.causal ? min(nkb, qb + 1) : nkb;
+        float part = 0.f;
+        for (int kb = lane; kb < kb_end; kb += 64)
+          part += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(crs, (uint32_t)((qs * nkb + kb) * 4), 0, 1));
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+        const float total = round_to<CT>(part);
+        uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * a.nqb + qb) * nkb;
+        for (int kb = lane; kb < nkb; kb += 64) {
+          const float cv = kb < kb_end ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                              crs, (uint32_t)((qs * nkb + kb) * 4), 0, 1))
+                                       : 0.f;
+          out[kb] = (uint16_t)(pack2<CT>(kb < kb_end ? cv / total : 0.f, 0.f) & 0xffffu);
+        }
+      }
     }
   }
 }
@@ -556,12 +616,22 @@ hipError_t launch_block_mass_pool(const PoolArgs& a, int dtype, int D, hipStream
 hipError_t launch_max_pool(const PoolArgs& a, int dtype, int D, hipStream_t stream) {
   (void)D;
   if (a.B * a.H * a.nqb == 0) return hipSuccess;
-  const int items = a.B * a.H * a.nqb;
+  const int items = a.B * a.H * ((a.Nq + 127) / 128);
   const int groups = min(items, max_pool_groups());
-  if (dtype == kBF16)
-    max_pool_persistent_kernel<kBF16><<<groups, 256, 0, stream>>>(a, items);
-  else
-    max_pool_persistent_kernel<kF16><<<groups, 256, 0, stream>>>(a, items);
+#define SA_MAXP(KB)                                                                  \
+  do {                                                                               \
+    if (dtype == kBF16)                                                              \
+      max_pool_persistent_kernel<kBF16, KB><<<groups, 256, 0, stream>>>(a, items);   \
+    else                                                                             \
+      max_pool_persistent_kernel<kF16, KB><<<groups, 256, 0, stream>>>(a, items);    \
+  } while (0)
+  switch (a.bs) {
+    case 16: SA_MAXP(16); break;
+    case 32: SA_MAXP(32); break;
+    case 64: SA_MAXP(64); break;
+    default: SA_MAXP(128); break;
+  }
+#undef SA_MAXP
   return hipGetLastError();
 }
 

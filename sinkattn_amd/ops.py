@@ -54,7 +54,8 @@ def _pad_head_dim(t: torch.Tensor, to: Optional[int] = None) -> torch.Tensor:
     return torch.nn.functional.pad(t, (0, mult - D % mult))
 
 
-# Block sizes of the matrix-core exact block-mass kernel (16-bit inputs, head dim 128).
+# Block sizes of the matrix-core pooling kernels (exact block mass and max-pool; 16-bit
+# inputs, head dim 128).
 MASS_MFMA_BLOCKS = (16, 32, 64, 128)
 
 
@@ -429,6 +430,11 @@ def max_pool_scores(q: torch.Tensor, k: torch.Tensor, sm_scale: float, block_siz
     if q.dtype != k.dtype:
         raise TypeError("q and k must share a dtype")
     dt = _lib.dtype_code(q.dtype)
+    if q.dtype != torch.float32 and D in (16, 32, 64) and int(block_size) in MASS_MFMA_BLOCKS:
+        # the reference's head dims below 128, zero-padded for the matrix-core kernel (the
+        # dot products, all the map depends on, are unchanged)
+        q, k = _pad_head_dim(q, 128), _pad_head_dim(k, 128)
+        D = 128
     qk, kk = _kernel_operand(q), _kernel_operand(k)
     nd = _cdiv(N, block_size)
     po = torch.empty((B, H, nd, nd), dtype=q.dtype, device=q.device)

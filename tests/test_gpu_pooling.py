@@ -177,6 +177,18 @@ def test_max_pool_persistent_loop_ragged():
         _max_pool_close(ours, ref, q, k, sm, causal=causal, what=f"causal={causal}")
 
 
+@pytest.mark.parametrize("bs", [16, 32, 64])
+def test_max_pool_small_blocks_persistent_loop_ragged(bs):
+    # the matrix-core max-pool kernel at blocks 16-64: 96 heads x 9 items of 128 rows (more
+    # than one item per resident work-group), N = 1100 (ragged last block), causal and not
+    q, k = _qk(1, 96, 1100, 1100, torch.bfloat16, seed=40 + bs, sinks=3)
+    sm = 1.0 / math.sqrt(128)
+    for causal in (False, True):
+        ours = ops.max_pool_scores(q.cuda(), k.cuda(), sm, block_size=bs, causal=causal).cpu()
+        ref = torch_ref.max_pool_map(q, k, sm, block_size=bs, causal=causal)
+        _max_pool_close(ours, ref, q, k, sm, bs, causal, what=f"bs={bs} causal={causal}")
+
+
 def test_max_pool_many_key_blocks():
     # N = 40000 -> 313 key blocks per row (ragged 64); three query blocks are checked
     # against the closed form.
