@@ -14,8 +14,13 @@ Printed as one JSON line:
   ms_per_step     ms per layer call
   roofline        the block_sparse_fwd kernel against the bf16 MFMA peak
   extra fields    dense-mask time of the same kernel, the calibration pooling pass
-                  (ms, TFLOP/s, "HBM GB/s" = algorithmic Q+K+map bytes / time) and the
-                  coverage-mask build (us) on the same shape
+                  (ms, TFLOP/s, "HBM GB/s" = algorithmic Q+K+map bytes / time, the
+                  fraction of its VALU roof from a probe of its per-score VALU mix, block
+                  64 times), the coverage-mask build (us) and plan (us, fresh and with the
+                  launch-order cache) on the same shape, the Z-Image layer (config 4, also
+                  in the reference processor's fresh-mask-per-call pattern), the 30-layer
+                  calibration pass (config 3), the 30 x 50 attention stack (config 5) and
+                  the config-1 chain beside the same steps on the host
   cpu_baseline    the oracle's fp32 block-gather masked softmax on the host, timed on
                   a bounded sample of q-blocks and scaled to the full layer
 """
@@ -31,9 +36,11 @@ import time
 MFMA_BF16_PEAK_TFLOPS = 2516.6
 HBM_PEAK_GBS = 8000.0
 NOMINAL_CLOCK_GHZ = 2.4
-# Shader clock of block_mass_persistent_kernel at the config-2 shape, from rocprofv3
-# --pmc GRBM_GUI_ACTIVE (cycles per dispatch / its duration): profiles/block_mass_pool_wan_c2.md.
-POOL_KERNEL_CLOCK_GHZ = 1.59
+# Shader-clock cycles one launch of block_mass_persistent_kernel takes at the config-2 shape:
+# rocprofv3 --pmc GRBM_GUI_ACTIVE summed over the 8 XCDs / 8 (profiles/block_mass_pool_wan_c2.md).
+# The count hardly moves between launches whose durations differ by 18% (the clock moves), so
+# the kernel's clock in a run is these cycles / the launch duration measured there.
+POOL_KERNEL_CYCLES = 1.173e7
 
 # HBM traffic per launch at the default workload (--density 0.20, the seeds below),
 # from rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (KiB per dispatch) scaled by what
@@ -41,7 +48,7 @@ POOL_KERNEL_CLOCK_GHZ = 1.59
 # 0.5 GiB for it -> x2.0, WRITE_SIZE reads 1 GiB -> x1.0).  Summaries with the commands:
 # profiles/block_sparse_fwd_wan_c2.md and profiles/block_mass_pool_wan_c2.md.
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
-TRAFFIC_KIB = {"fa": (1449431.0, 199631.0), "pool": (1278539.0, 792577.0)}
+TRAFFIC_KIB = {"fa": (1464336.0, 199631.0), "pool": (1278117.0, 792577.0)}
 
 
 def traffic_bytes(kind):
@@ -60,7 +67,8 @@ def _parse():
     p.add_argument("--no-extras", action="store_true", help="skip dense/pooling/mask timings")
     p.add_argument("--cpu-sample-qblocks", type=int, default=0,
                    help="q-blocks of the layer the CPU baseline times (0 = the whole layer, 6144)")
-    p.add_argument("--only", choices=["all", "fa", "fa4", "pool", "maxpool", "mask"], default="all",
+    p.add_argument("--only", choices=["all", "fa", "fa4", "pool", "pool64", "maxpool", "maxpool64", "mask"],
+                   default="all",
                    help="profiling aid: run just one kernel family (no JSON line unless 'all')")
     p.add_argument("--copy-mb", type=int, default=0,
                    help="profiling aid: first run a device copy of this many MiB (counter calibration)")
@@ -267,7 +275,8 @@ def valu_roof(torch, dev, pool_ms, scores):
     (sinkattn_amd/csrc/probe/valu_mix.hip) issues exactly that mix at the pooling kernel's
     occupancy and gives the rate a CU retires it at, per shader clock (clock from the
     probe's own s_memtime / s_memrealtime stamps).  roof_ms = scores / (rate * CUs * clock)
-    at the nominal 2.4 GHz and at the pooling kernel's profiled clock."""
+    at the nominal 2.4 GHz and at the pooling kernel's own clock in this run (its profiled
+    cycles per launch / the measured launch time)."""
     import ctypes
     from sinkattn_amd import build as sbuild
     lib = ctypes.CDLL(str(sbuild.PROBE_PATH))
@@ -292,15 +301,17 @@ def valu_roof(torch, dev, pool_ms, scores):
     n = blocks * 256 * reps * chains
     rate = n / (ms * 1e-3) / clock_hz / cus        # scores per shader clock per CU
     roof_nom = scores / (rate * cus * NOMINAL_CLOCK_GHZ * 1e9) * 1e3
-    roof_k = scores / (rate * cus * POOL_KERNEL_CLOCK_GHZ * 1e9) * 1e3
+    kclock_ghz = POOL_KERNEL_CYCLES / (pool_ms * 1e-3) / 1e9
+    roof_k = scores / (rate * cus * kclock_ghz * 1e9) * 1e3
     return {"bound": "valu", "mix_per_score": "v_fma_f32 + v_exp_f32 + v_add_f32",
             "scores_per_launch": scores,
             "probe_scores_per_clock_per_cu": round(rate, 2), "probe_clock_ghz": round(clock_hz / 1e9, 3),
             "roof_ms_at_nominal_clock": round(roof_nom, 3), "frac_at_nominal_clock": round(roof_nom / pool_ms, 4),
-            "kernel_clock_ghz_profiled": POOL_KERNEL_CLOCK_GHZ,
+            "kernel_clock_ghz": round(kclock_ghz, 3),
             "roof_ms_at_kernel_clock": round(roof_k, 3), "frac_at_kernel_clock": round(roof_k / pool_ms, 4),
-            "note": "fraction = VALU-roof time / measured pooling time; the clock of the pooling kernel "
-                    "comes from rocprofv3 GRBM_GUI_ACTIVE (profiles/block_mass_pool_wan_c2.md)"}
+            "note": "fraction = VALU-roof time / measured pooling time; the kernel's clock = its cycles per "
+                    "launch from rocprofv3 GRBM_GUI_ACTIVE (profiles/block_mass_pool_wan_c2.md) / this "
+                    "run's launch time"}
 
 
 def main():
@@ -345,7 +356,9 @@ def main():
         kernel_call = lambda: ops.block_sparse_attention(qz, kz, vz, zplan)  # noqa: E731
     if args.only != "all":
         fn = {"fa": kernel_call, "fa4": kernel_call, "pool": lambda: ops.block_mass_scores(q, k),
+              "pool64": lambda: ops.block_mass_scores(q, k, 64),
               "maxpool": lambda: ops.max_pool_scores(q, k, 1.0 / math.sqrt(D)),
+              "maxpool64": lambda: ops.max_pool_scores(q, k, 1.0 / math.sqrt(D), 64),
               "mask": lambda: ops.coverage_mask(torch.rand(H, 256, 256, device=dev), 0.85, True)}[args.only]
         for _ in range(args.warmup + args.steps):
             fn()
@@ -426,6 +439,10 @@ def main():
         mms = time_fn(torch, lambda: ops.max_pool_scores(q, k, 1.0 / math.sqrt(D)), 3, 1)
         out["pooling"]["max_pool_ms"] = round(mms, 3)
         out["pooling"]["max_pool_tflops"] = round(pool_flops / (mms * 1e-3) / 1e12, 2)
+        # the calibration CLIs' --block_size 64 (wanx/offline/calibrate_sink_sparse.py:97)
+        out["pooling"]["block64_ms"] = round(time_fn(torch, lambda: ops.block_mass_scores(q, k, 64), 3, 1), 3)
+        out["pooling"]["max_pool_block64_ms"] = round(
+            time_fn(torch, lambda: ops.max_pool_scores(q, k, 1.0 / math.sqrt(D), 64), 3, 1), 3)
         # the full Wan layer call with the default compensation branch (pooled_kv, gap 30,
         # adaptive mix): fused kernel vs the reference's three steps on this build's kernels
         gap = 30
@@ -549,16 +566,21 @@ def zimage_layer(torch, dev, ops, sa, args):
         rm = zr._slice_runtime_sink_mask(pkg, image_blocks=128, current_text_blocks=4, total_blocks=132)
         return zr._force_text_dense_runtime_mask(rm, image_blocks=128, current_text_blocks=4).unsqueeze(0)
 
-    fresh_ms = time_fn(torch, lambda: sa._block_sparse_attn(q, k, v, runtime_mask(), return_lse=False),
-                       args.steps, args.warmup)
-    cached_ms = time_fn(torch, lambda: sa._block_sparse_attn(q, k, v, mask, return_lse=False),
-                        args.steps, args.warmup)
-    # the drop-in's own part: a mask tensor it has not seen (new object, same content) per call
-    fresh = [mask.clone() for _ in range(args.steps + args.warmup)]
-    it = iter(fresh)
-    tensor_ms = time_fn(torch, lambda: sa._block_sparse_attn(q, k, v, next(it), return_lse=False),
-                        args.steps, args.warmup)
-    del fresh
+    # three alternating rounds of (cached mask object, new mask object, processor pattern),
+    # medians, so that clock drift between the loops does not enter the comparison
+    cached_r, tensor_r, fresh_r = [], [], []
+    for _ in range(3):
+        cached_r.append(time_fn(torch, lambda: sa._block_sparse_attn(q, k, v, mask, return_lse=False),
+                                args.steps, args.warmup))
+        # the drop-in's own part: a mask tensor it has not seen (new object, same content) per call
+        fresh = [mask.clone() for _ in range(args.steps + args.warmup)]
+        it = iter(fresh)
+        tensor_r.append(time_fn(torch, lambda: sa._block_sparse_attn(q, k, v, next(it), return_lse=False),
+                                args.steps, args.warmup))
+        del fresh, it
+        fresh_r.append(time_fn(torch, lambda: sa._block_sparse_attn(q, k, v, runtime_mask(), return_lse=False),
+                               args.steps, args.warmup))
+    cached_ms, tensor_ms, fresh_ms = (sorted(x)[1] for x in (cached_r, tensor_r, fresh_r))
     mops_us = gpu_time_fn(torch, runtime_mask, 20, 5) * 1e3
     return {"pooling_ms": round(pms, 3), "pooling_tflops": round(pool_flops / (pms * 1e-3) / 1e12, 2),
             "mask_us": round(mus, 1), "mask_density": round(mask.float().mean().item(), 4),
