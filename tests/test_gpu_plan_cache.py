@@ -166,3 +166,39 @@ def test_plan_cached_rejects_bad_arguments():
         ops.block_sparse_plan(m, small, 4)
     with pytest.raises(ValueError):
         ops.block_sparse_plan(m, torch.zeros(ops.order_cache_ints(1, 2, 8, 4), dtype=torch.int64, device="cuda"), 4)
+
+
+def test_cached_plan_over_the_interleaved_fallback():
+    # More than 4096 chunks (4100 heads of 20 q-blocks): the plan's interleaved fallback has no
+    # chunk table, and the cached plan gives the same lists and slots as the plain one
+    B, H, nqb = 1, 4100, 20
+    m = _mask(B, H, nqb, nqb, 0.3, seed=70)
+    ref = ops.block_sparse_plan(m)
+    cache = torch.zeros(ops.order_cache_ints(B, H, nqb, 2), dtype=torch.int32, device="cuda")
+    for _ in range(2):
+        p = ops.block_sparse_plan(m.clone(), cache, 2)
+        torch.cuda.synchronize()
+        assert torch.equal(p.counts, ref.counts) and torch.equal(p.order, ref.order)
+
+
+def test_drop_in_on_a_side_stream_with_new_mask_tensors():
+    # the drop-in keeps a launch-order cache per stream; calls on a side stream, each with a new
+    # mask tensor, give the outputs of the uncached plan
+    B, H, N = 1, 3, 1500
+    nb = math.ceil(N / 128)
+    g = torch.Generator().manual_seed(8)
+    q, k, v = (torch.randn(B, H, N, 128, generator=g).to("cuda", torch.bfloat16) for _ in range(3))
+    m = _mask(B, H, nb, nb, 0.3, seed=9, dense_rows=(2,))
+    want, wl = ops.block_sparse_attention(q, k, v, ops.block_sparse_plan(m))
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    outs = []
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            o, l = sa._block_sparse_attn(q, k, v, m.clone())
+            outs.append((o, l))
+    torch.cuda.synchronize()
+    for o, l in outs:
+        assert torch.equal(o.view(torch.int16), want.view(torch.int16))
+        assert torch.equal(l[..., 0], wl.to(l.dtype))
