@@ -166,47 +166,53 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_kernel(FwdArgs a) {
 // ------------------------------------------------------------------------------------
 // D = 128, bf16/f16: K and V tiles go global -> LDS by buffer DMA (no staging
 // registers; rows >= Nk read as zero through the buffer bounds), and V^T is read from
-// the row-major V tile with the gfx950 transpose read ds_read_b64_tr_b16.  K and V are
-// staged against each other: V(i)'s copies are spread over S(i), one per k-step, and
-// K(i+1)'s over softmax(i), one per step, so that the copies of the four waves never
-// queue up at the CU's vector-memory pipe in one burst; three work-group barriers per tile
-// (K free, V landed, V free and K(i+1) landed).  LDS layout: 128 rows x 16 chunks of 16 bytes per tile,
-// physical chunk = logical ^ (row & 15) for K and logical ^ (4 * (row & 3)) for V, which
-// keeps the 16-lane K reads and the 32-lane transpose reads on distinct banks.
+// the row-major V tile with the gfx950 transpose read ds_read_b64_tr_b16.  Both products
+// run on v_mfma_f32_16x16x32, which with random 16-bit operands draws less power per flop
+// than 32x32x16, so the power-limited chip holds a higher clock.  A wave's 32 query rows
+// are two 16-column tiles qt:
+//     S^T[16 kt .. +16, qt] = K Q^T        (A = 16 K rows from LDS, B = Q^T in VGPRs)
+//     O^T[16 dt .. +16, qt] += V^T P^T     (A = V^T by transpose reads, B = P^T)
+// Lane l holds query 16 qt + l % 16 in both products; its S^T registers (kt, qt) hold keys
+// 16 kt + 4 (l / 16) + i, i < 4.  A PV k-step kc of 32 keys takes its eight B values from
+// S^T tiles (2 kc, qt) and (2 kc + 1, qt), and the transpose reads pick the same keys for
+// the A operand, so P never leaves the registers.  K and V are staged against each other:
+// V(i)'s copies are spread over S(i) and K(i+1)'s over softmax(i), one per step, so that
+// the copies of the four waves never queue up at the CU's vector-memory pipe in one burst;
+// three work-group barriers per tile (K free, V landed, V free and K(i+1) landed).  LDS
+// layout: 128 rows x 16 chunks of 16 bytes per tile, physical chunk = logical ^ (row & 15)
+// for K (a 16-lane K read touches 16 distinct chunks) and logical ^ 2 (row & 7) for V (a
+// half-wave transpose read touches 8 distinct 32-byte column pairs).
 // ------------------------------------------------------------------------------------
 constexpr float kLazyRescaleLog2 = 8.0f;
 
-// Per-lane LDS addresses of the d128 tile loop (bytes): the DMA destination offsets of this
-// wave's copies, the K rows of the S^T A operand, and the V^T transpose reads.
+// Per-lane LDS addresses of the d128 tile loop (bytes).
 struct D128Lanes {
   uint32_t k_off, v_off;  // global byte offset of this lane's first 16-byte DMA chunk
-  uint32_t ka[8];         // K: MFMA row t*32 + k_row_perm(l32), chunk 2ds + hl (+ t * 8192)
-  uint32_t va[4][2];      // V^T transpose reads of d-tile dt
+  uint32_t ka[4];         // K A operand of k-step ks: row l % 16 (+ 16 kt), chunk 4 ks + l / 16
+  uint32_t va[8];         // V^T transpose reads of d-tile dt (+ 32 kc rows, + 16 h rows)
 };
 
 __device__ __forceinline__ D128Lanes d128_lanes(int wave, int lane, uint32_t kstride, uint32_t vstride) {
   D128Lanes L;
-  const int hl = lane >> 5, l32 = lane & 31;
+  const int g = lane >> 4, sl = lane & 15;
   // DMA: instruction j of wave w fills tile rows 16j + 4w + lane/16 (LDS bytes
   // [(256j + 64w) * 16, +1024)); the swizzle of those rows does not depend on j.
-  const int drow = 4 * wave + (lane >> 4);
-  L.k_off = (uint32_t)drow * kstride + (uint32_t)(((lane & 15) ^ (drow & 15)) * 16);
-  L.v_off = (uint32_t)drow * vstride + (uint32_t)(((lane & 15) ^ (4 * (drow & 3))) * 16);
-  const int prow = k_row_perm(l32);
+  const int drow = 4 * wave + g;
+  L.k_off = (uint32_t)drow * kstride + (uint32_t)((sl ^ (drow & 15)) * 16);
+  L.v_off = (uint32_t)drow * vstride + (uint32_t)((sl ^ (2 * (drow & 7))) * 16);
 #pragma unroll
-  for (int ds = 0; ds < 8; ++ds) L.ka[ds] = (uint32_t)(prow * 256 + (((2 * ds + hl) ^ (prow & 15)) * 16));
-  // V^T via transpose reads: 16-lane group g, lane s in group -> source row
-  // 8*(g/2) + 4r + s/4 (+16u + 32t), columns dt*32 + 16*(g%2) + 4*(s%4) .. +3.
-  const int g = lane >> 4, sl = lane & 15;
+  for (int ks = 0; ks < 4; ++ks) L.ka[ks] = (uint32_t)(sl * 256 + (((4 * ks + g) ^ sl) * 16));
+  // Transpose read h of d-tile dt at k-step kc: lane s of 16-lane group g points at key row
+  // 32 kc + 16 h + 4 g + s / 4, columns 16 dt + 4 (s % 4) .. +3.  Lane l of the group then
+  // receives element l % 4 of the rows of lanes 4 j + (l % 16) / 4, j < 4: d = 16 dt + l % 16
+  // at keys 32 kc + 16 h + 4 g + j, the keys of B slots 4 h + j.
+  const int row = 4 * g + (sl >> 2);  // + 32 kc + 16 h, which leave row & 7 unchanged
+  const int a4 = sl & 3;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int row = 8 * (g >> 1) + 4 * r + (sl >> 2);
-      const int chunk = dt * 4 + 2 * (g & 1) + ((sl & 3) >> 1);
-      const int phys = chunk ^ (4 * (row & 3));
-      L.va[dt][r] = (uint32_t)(row * 256 + phys * 16 + (sl & 1) * 8);
-    }
+  for (int dt = 0; dt < 8; ++dt) {
+    const int chunk = 2 * dt + (a4 >> 1);
+    L.va[dt] = (uint32_t)(row * 256 + ((chunk ^ (2 * (row & 7))) * 16) + (a4 & 1) * 8);
+  }
   return L;
 }
 
@@ -228,43 +234,49 @@ __device__ __forceinline__ void d128_copy_tile(SA_LDS char* dst, const char* bas
 
 // One 128-key tile of the d128 loop for this wave's 32 query rows:
 //   S^T = K Q^T from the K tile, with vcopy(j) (this tile's V copy j into the V buffer, free
-//   since the previous tile's B2) after the MFMAs of k-step j; barrier B1 (every wave is
-//   done with K); the online softmax with kcopy(j) (the next tile's K copy j into the K
-//   buffer) after step j; barrier BV (every wave's V copies have landed: vmcnt(8) leaves
-//   only the eight K copies issued after them in flight); O^T += V^T P^T from the V tile;
-//   barrier B2 (the next K has landed, every wave is done with V).  kcopy must issue a copy
-//   for every j, also after the last tile (then from a 0-byte buffer), so that the count
-//   of BV holds.
+//   since the previous tile's B2) after every fourth (k-step, key tile) pair; barrier B1
+//   (every wave is done with K); the online softmax with kcopy(j) (the next tile's K copy j
+//   into the K buffer) after step j; barrier BV (every wave's V copies have landed: vmcnt(8)
+//   leaves only the eight K copies issued after them in flight); O^T += V^T P^T from the V
+//   tile; barrier B2 (the next K has landed, every wave is done with V).  kcopy must issue a
+//   copy for every j, also after the last tile (then from a 0-byte buffer), so that the
+//   count of BV holds.
 // Keys at or past klim are masked; bias is added to the log2-domain logits (compensation
-// tiles); c = softmax scale * log2(e).
+// tiles); c = softmax scale * log2(e).  g = lane / 16.
 template <int CT, typename FV, typename FK>
 __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, const D128Lanes& L,
-                                          const u32x4 (&qf)[8], int key0, int klim, float bias,
-                                          float c, int hl, f32x16 (&o)[4], float& m_run,
-                                          float& l_run, FV&& vcopy, FK&& kcopy) {
-  constexpr int DS = 8, DT = 4;
-  f32x16 s[4];
+                                          const u32x4 (&qf)[2][4], int key0, int klim, float bias,
+                                          float c, int g, f32x4 (&o)[8][2], float (&m_run)[2],
+                                          float (&l_run)[2], FV&& vcopy, FK&& kcopy) {
+  constexpr int KR = 4;  // K reads issued ahead of their MFMAs
+  constexpr int VR = 3;  // transpose-read pairs issued ahead of their MFMAs
+  f32x4 s[8][2];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) s[t] = f32x16{};
+  for (int kt = 0; kt < 8; ++kt) {
+    s[kt][0] = f32x4{};
+    s[kt][1] = f32x4{};
+  }
   {
-    u32x4 kr[2][4];
+    // pair p = 8 ks + kt: one K read (rows 16 kt .., d slice ks), the MFMAs of both q tiles
+    u32x4 kr[32];
+    auto kread = [&](int p) { return *(SA_LDS const u32x4*)(lk + L.ka[p >> 3] + (p & 7) * 4096); };
 #pragma unroll
-    for (int t = 0; t < 4; ++t) kr[0][t] = *(SA_LDS const u32x4*)(lk + L.ka[0] + t * 8192);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    for (int p = 0; p < KR; ++p) kr[p] = kread(p);
+    __builtin_amdgcn_sched_group_barrier(0x100, KR, 0);
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        s[t] = mfma32x32x16<CT>(kr[ds & 1][t], qf[ds], s[t]);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (ds + 1 < DS) {
-          kr[(ds + 1) & 1][t] = *(SA_LDS const u32x4*)(lk + L.ka[ds + 1] + t * 8192);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        if (t == 1) {
-          vcopy(ds);  // V copy ds of this tile, one per k-step
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        }
+    for (int p = 0; p < 32; ++p) {
+      const int ks = p >> 3, kt = p & 7;
+      s[kt][0] = mfma16x16x32<CT>(kr[p], qf[0][ks], s[kt][0]);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (p + KR < 32) {
+        kr[p + KR] = kread(p + KR);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      s[kt][1] = mfma16x16x32<CT>(kr[p], qf[1][ks], s[kt][1]);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if ((p & 3) == 3) {
+        vcopy(p >> 2);  // V copy of this tile, one per four pairs
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       }
     }
   }
@@ -274,40 +286,51 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
 
   if (key0 + 128 > klim) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (key0 + t * 32 + tile_key(hl, j) >= klim) s[t][j] = neg_inf();
+      for (int i = 0; i < 4; ++i)
+        if (key0 + 16 * kt + 4 * g + i >= klim) {
+          s[kt][0][i] = neg_inf();
+          s[kt][1][i] = neg_inf();
+        }
   }
-  float mx = neg_inf();
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int qt = 0; qt < 2; ++qt) {
+    float mx = neg_inf();
 #pragma unroll
-    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[t][j]);
-  mx = max_xor32(mx);
-  const float m_tile = __builtin_fmaf(mx, c, bias);
-  if (m_tile > m_run + kLazyRescaleLog2) {
-    const float alpha = fast_exp2(m_run - m_tile);
-    l_run *= alpha;
+    for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-    for (int i = 0; i < DT; ++i) o[i] *= alpha;
-    m_run = m_tile;
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][qt][i]);
+    mx = max_col16(mx);
+    const float m_tile = __builtin_fmaf(mx, c, bias);
+    if (m_tile > m_run[qt] + kLazyRescaleLog2) {
+      const float alpha = fast_exp2(m_run[qt] - m_tile);
+      l_run[qt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt][qt] *= alpha;
+      m_run[qt] = m_tile;
+    }
   }
   u32x4 p[4][2];
-  float lsum[4] = {0.f, 0.f, 0.f, 0.f};
-  auto make_p = [&](int t, int u) {
+  float lsum[4][2];
+  auto make_p = [&](int kc, int qt) {
+    const float nb = bias - m_run[qt];
+    float acc = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float v0 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e], c, bias - m_run));
-      const float v1 = fast_exp2(__builtin_fmaf(s[t][8 * u + 2 * e + 1], c, bias - m_run));
-      p[t][u][e] = pack2<CT>(v0, v1);
-      lsum[t] += v0 + v1;
-    }
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float v0 = fast_exp2(__builtin_fmaf(s[2 * kc + h][qt][2 * e], c, nb));
+        const float v1 = fast_exp2(__builtin_fmaf(s[2 * kc + h][qt][2 * e + 1], c, nb));
+        p[kc][qt][2 * h + e] = pack2<CT>(v0, v1);
+        acc += v0 + v1;
+      }
+    lsum[kc][qt] = acc;
   };
-  auto vread = [&](int dt, int t, int u) -> u32x4 {
-    const uint32_t off = t * 8192 + u * 4096;
-    const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + L.va[dt][0] + off));
-    const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(lv + L.va[dt][1] + off));
+  auto vread = [&](int r) -> u32x4 {  // r = 8 kc + dt
+    SA_LDS char* base = lv + L.va[r & 7] + (r >> 3) * 8192;
+    const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)base);
+    const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SA_LDS v4i16*)(base + 4096));
     const u32x2 y0 = __builtin_bit_cast(u32x2, x0), y1 = __builtin_bit_cast(u32x2, x1);
     return u32x4{y0[0], y0[1], y1[0], y1[1]};
   };
@@ -324,27 +347,26 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_s_setprio(1);
   {
-    u32x4 vr[2][DT];
+    // pair r = 8 kc + dt: two transpose reads (d tile dt, keys of k-step kc), both q tiles
+    u32x4 vr[32];
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) vr[0][dt] = vread(dt, 0, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    for (int r = 0; r < VR; ++r) vr[r] = vread(r);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * VR, 0);
 #pragma unroll
-    for (int step = 0; step < 8; ++step) {
-      const int t = step >> 1, u = step & 1;
-      const int nt = (step + 1) >> 1, nu = (step + 1) & 1;
-      if (step + 1 < 8) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) vr[(step + 1) & 1][dt] = vread(dt, nt, nu);
+    for (int r = 0; r < 32; ++r) {
+      const int kc = r >> 3, dt = r & 7;
+      o[dt][0] = mfma16x16x32<CT>(vr[r], p[kc][0], o[dt][0]);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (r + VR < 32) {
+        vr[r + VR] = vread(r + VR);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        o[dt] = mfma32x32x16<CT>(vr[step & 1][dt], p[t][u], o[dt]);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (step + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
+      o[dt][1] = mfma16x16x32<CT>(vr[r], p[kc][1], o[dt][1]);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
   }
-  l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) l_run[qt] += (lsum[0][qt] + lsum[1][qt]) + (lsum[2][qt] + lsum[3][qt]);
   __builtin_amdgcn_s_setprio(0);
   drain_then_barrier();  // B2: next K landed, every wave done with V
 }
@@ -396,27 +418,32 @@ __device__ __forceinline__ void d128_issue_k(const D128Item& it, int key0, int k
   d128_copy_tile(lk, base, kstride, klim - key0, L.k_off, wave);
 }
 
-// O of this wave's 32 rows through its 8 KB of an idle LDS tile buffer: each lane holds
-// 4-value pieces of its own row, so after the transpose every store instruction writes 4
-// whole 256-byte rows.  The caller guarantees that no wave reads the buffer and no copy
-// into it is in flight; each wave touches only its own slice.
+// O of this wave's 32 rows through its 8 KB of an idle LDS tile buffer: lane l holds d values
+// 16 dt + 4 (l / 16) .. +3 of row 16 qt + l % 16, written as 8-byte pieces; after the
+// transpose every store instruction writes 4 whole 256-byte rows.  The caller guarantees that
+// no wave reads the buffer and no copy into it is in flight; each wave touches only its own
+// slice.
 template <int CT>
-__device__ __forceinline__ void d128_store_o_staged(const FwdArgs& a, const D128Item& it, const f32x16 (&o)[4],
-                                                    float m_run, float l_run, SA_LDS char* buf, int wave,
-                                                    int lane) {
-  const int hl = lane >> 5, l32 = lane & 31;
-  const float l = sum_xor32(l_run);
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+__device__ __forceinline__ void d128_store_o_staged(const FwdArgs& a, const D128Item& it, const f32x4 (&o)[8][2],
+                                                    const float (&m_run)[2], const float (&l_run)[2],
+                                                    SA_LDS char* buf, int wave, int lane) {
+  const int g = lane >> 4, sl = lane & 15;
+  float l[2], inv[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    l[qt] = sum_col16(l_run[qt]);
+    inv[qt] = l[qt] > 0.f ? 1.f / l[qt] : 0.f;
+  }
   SA_LDS char* ob = buf + wave * 8192;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int chunk = (dt * 4 + g) ^ (l32 & 15);
+    for (int dt = 0; dt < 8; ++dt) {
+      const int chunk = (2 * dt + (g >> 1)) ^ sl;  // row 16 qt + sl: row & 15 == sl
       u32x2 w;
-      w[0] = pack2<CT>(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv);
-      w[1] = pack2<CT>(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
-      *(SA_LDS u32x2*)(ob + l32 * 256 + chunk * 16 + hl * 8) = w;
+      w[0] = pack2<CT>(o[dt][qt][0] * inv[qt], o[dt][qt][1] * inv[qt]);
+      w[1] = pack2<CT>(o[dt][qt][2] * inv[qt], o[dt][qt][3] * inv[qt]);
+      *(SA_LDS u32x2*)(ob + (16 * qt + sl) * 256 + chunk * 16 + (g & 1) * 8) = w;
     }
   __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0) only
   const int bh = it.item / a.nqb;
@@ -430,9 +457,14 @@ __device__ __forceinline__ void d128_store_o_staged(const FwdArgs& a, const D128
     if (q0 + rr < a.Nq)
       *reinterpret_cast<u32x4*>(obase + ((int64_t)(q0 + rr) * a.os[2]) * 2 + cc * 16) = val;
   }
-  const int qrow = q0 + l32;
-  if (qrow < a.Nq && a.lse != nullptr && hl == 0)
-    a.lse[((int64_t)b * a.H + h) * a.Nq + qrow] = it.ntot > 0 ? (m_run + __log2f(l)) * kLn2 : pos_inf();
+  if (a.lse != nullptr && g == 0) {
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const int qrow = q0 + 16 * qt + sl;
+      if (qrow < a.Nq)
+        a.lse[((int64_t)b * a.H + h) * a.Nq + qrow] = it.ntot > 0 ? (m_run[qt] + __log2f(l[qt])) * kLn2 : pos_inf();
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------
@@ -445,7 +477,7 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hl = lane >> 5, l32 = lane & 31;
+  const int g = lane >> 4, sl = lane & 15;
   const int item = __builtin_amdgcn_readfirstlane(a.order ? a.order[blockIdx.x] : (int)blockIdx.x);
   if (item < 0) return;
   const D128Item it = d128_item(a, item);
@@ -454,15 +486,24 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
   SA_LDS char* lk = (SA_LDS char*)lds_k;
   SA_LDS char* lv = (SA_LDS char*)lds_v;
 
-  const int qrow = it.qb * 128 + wave * 32 + l32;
-  u32x4 qf[8];
-  load_q_operand<CT, CT, 128>(qf, it.qbase, a.qs[2], qrow, a.Nq, hl);
-
-  f32x16 o[4];
+  // Q^T B operands: query 16 qt + l % 16 of the wave's rows, d slice 32 ks + 8 (l / 16)
+  u32x4 qf[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
-  float m_run = neg_inf();
-  float l_run = 0.f;
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qrow = it.qb * 128 + wave * 32 + 16 * qt + sl;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qf[qt][ks] = qrow < a.Nq ? *(const u32x4*)(it.qbase + ((int64_t)qrow * a.qs[2] + 32 * ks + 8 * g) * 2)
+                               : u32x4{0, 0, 0, 0};
+  }
+  f32x4 o[8][2];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    o[dt][0] = f32x4{};
+    o[dt][1] = f32x4{};
+  }
+  float m_run[2] = {neg_inf(), neg_inf()};
+  float l_run[2] = {0.f, 0.f};
   const float c = a.scale * kLog2e;
 
   // kernel arguments the tile loop needs, read once
@@ -486,7 +527,7 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
     // access), so that every tile issues the same copies and waits
     const __amdgpu_buffer_rsrc_t krs = make_rsrc((comp_next ? it.kdbase : it.kbase) + (int64_t)key0_next * kstride,
                                                  next ? (uint32_t)(klim_next - key0_next) * kstride : 0u);
-    d128_tile<CT>(lk, lv, L, qf, key0, klim, t < it.cnt ? 0.f : comp_bias, c, hl, o, m_run, l_run,
+    d128_tile<CT>(lk, lv, L, qf, key0, klim, t < it.cnt ? 0.f : comp_bias, c, g, o, m_run, l_run,
                   [&](int j) { d128_copy_one(lv, vrs, vstride, L.v_off, wave, j); },
                   [&](int j) { d128_copy_one(lk, krs, kstride, L.k_off, wave, j); });
     key0 = key0_next;

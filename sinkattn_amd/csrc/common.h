@@ -62,6 +62,23 @@ __device__ __forceinline__ f32x16 mfma32x32x16<kF16>(u32x4 a, u32x4 b, f32x16 c)
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// 16x16x32 MFMA, A/B as 8 packed 16-bit values in a u32x4.  Lane l holds row (A) or column
+// (B) l % 16 and the 8 contraction elements of slice l / 16; D holds column l % 16, rows
+// 4 (l / 16) .. +3.  With random 16-bit operands the matrix cores draw less power per flop in
+// this shape than in 32x32x16 and the chip holds a higher clock.
+template <int CT>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x32<kBF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x32<kF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
 // Reductions over lane pairs (l, l ^ 32), the two halves of a 32x32 MFMA column, with one
 // v_permlane32_swap (a VALU op, no LDS round trip).  The swap of x with itself leaves
 // (x[l], x[l + 32]) in lane l < 32 and (x[l - 32], x[l]) in lane l >= 32, so both lanes of a
@@ -77,6 +94,22 @@ __device__ __forceinline__ float max_xor32(float x) {
 __device__ __forceinline__ float sum_xor32(float x) {
   const f32x2 p = pair32(x);
   return p[0] + p[1];
+}
+
+// The same over lane pairs (l, l ^ 16) with v_permlane16_swap: lane l of an even 16-lane row
+// gets (x[l], x[l + 16]), lane l of an odd row (x[l - 16], x[l]).  Together with the pair32
+// forms they reduce over the four lanes l % 16 + 16 j of a 16x16 MFMA column.
+__device__ __forceinline__ f32x2 pair16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return f32x2{__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ float max_col16(float x) {
+  const f32x2 p = pair16(x);
+  return max_xor32(fmaxf(p[0], p[1]));
+}
+__device__ __forceinline__ float sum_col16(float x) {
+  const f32x2 p = pair16(x);
+  return sum_xor32(p[0] + p[1]);
 }
 
 // Load 8 consecutive elements of type IT at p (16-byte aligned for 16-bit types,
