@@ -175,7 +175,11 @@ __global__ __launch_bounds__(256) void block_sparse_fwd_kernel(FwdArgs a) {
 // Lane l holds query 16 qt + l % 16 in both products; its S^T registers (kt, qt) hold keys
 // 16 kt + 4 (l / 16) + i, i < 4.  A PV k-step kc of 32 keys takes its eight B values from
 // S^T tiles (2 kc, qt) and (2 kc + 1, qt), and the transpose reads pick the same keys for
-// the A operand, so P never leaves the registers.  K and V are staged against each other:
+// the A operand, so P never leaves the registers.  The row sums come from the matrix cores as
+// well: one more MFMA per k-step and q tile with an all-ones A operand sums the 16-bit P values
+// the PV product uses (O / l is then a weighted mean with weights that sum to one; l is within
+// 2^-8 relative of the fp32 sum for bf16, 2^-11 for f16), which keeps 64 adds per tile off
+// the VALU.  K and V are staged against each other:
 // V(i)'s copies are spread over S(i) and K(i+1)'s over softmax(i), one per step, so that
 // the copies of the four waves never queue up at the CU's vector-memory pipe in one burst;
 // three work-group barriers per tile (K free, V landed, V free and K(i+1) landed).  LDS
@@ -247,7 +251,7 @@ template <int CT, typename FV, typename FK>
 __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, const D128Lanes& L,
                                           const u32x4 (&qf)[2][4], int key0, int klim, float bias,
                                           float c, int g, f32x4 (&o)[8][2], float (&m_run)[2],
-                                          float (&l_run)[2], FV&& vcopy, FK&& kcopy) {
+                                          f32x4 (&l_acc)[2], FV&& vcopy, FK&& kcopy) {
   constexpr int KR = 4;  // K reads issued ahead of their MFMAs
   constexpr int VR = 3;  // transpose-read pairs issued ahead of their MFMAs
   f32x4 s[8][2];
@@ -305,17 +309,15 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
     const float m_tile = __builtin_fmaf(mx, c, bias);
     if (m_tile > m_run[qt] + kLazyRescaleLog2) {
       const float alpha = fast_exp2(m_run[qt] - m_tile);
-      l_run[qt] *= alpha;
+      l_acc[qt] *= alpha;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) o[dt][qt] *= alpha;
       m_run[qt] = m_tile;
     }
   }
   u32x4 p[4][2];
-  float lsum[4][2];
   auto make_p = [&](int kc, int qt) {
     const float nb = bias - m_run[qt];
-    float acc = 0.f;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -323,9 +325,7 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
         const float v0 = fast_exp2(__builtin_fmaf(s[2 * kc + h][qt][2 * e], c, nb));
         const float v1 = fast_exp2(__builtin_fmaf(s[2 * kc + h][qt][2 * e + 1], c, nb));
         p[kc][qt][2 * h + e] = pack2<CT>(v0, v1);
-        acc += v0 + v1;
       }
-    lsum[kc][qt] = acc;
   };
   auto vread = [&](int r) -> u32x4 {  // r = 8 kc + dt
     SA_LDS char* base = lv + L.va[r & 7] + (r >> 3) * 8192;
@@ -363,10 +363,18 @@ __device__ __forceinline__ void d128_tile(SA_LDS char* lk, SA_LDS char* lv, cons
       }
       o[dt][1] = mfma16x16x32<CT>(vr[r], p[kc][1], o[dt][1]);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (dt == 7) {
+        // row sums of the 16-bit P of this k-step: A = all ones, so every row of the product
+        // is the column sum, and every lane holds its query's running sum
+        const uint32_t one = CT == kBF16 ? 0x3F803F80u : 0x3C003C00u;
+        const u32x4 ones = {one, one, one, one};
+        l_acc[0] = mfma16x16x32<CT>(ones, p[kc][0], l_acc[0]);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        l_acc[1] = mfma16x16x32<CT>(ones, p[kc][1], l_acc[1]);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
     }
   }
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) l_run[qt] += (lsum[0][qt] + lsum[1][qt]) + (lsum[2][qt] + lsum[3][qt]);
   __builtin_amdgcn_s_setprio(0);
   drain_then_barrier();  // B2: next K landed, every wave done with V
 }
@@ -425,13 +433,13 @@ __device__ __forceinline__ void d128_issue_k(const D128Item& it, int key0, int k
 // slice.
 template <int CT>
 __device__ __forceinline__ void d128_store_o_staged(const FwdArgs& a, const D128Item& it, const f32x4 (&o)[8][2],
-                                                    const float (&m_run)[2], const float (&l_run)[2],
+                                                    const float (&m_run)[2], const f32x4 (&l_acc)[2],
                                                     SA_LDS char* buf, int wave, int lane) {
   const int g = lane >> 4, sl = lane & 15;
   float l[2], inv[2];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    l[qt] = sum_col16(l_run[qt]);
+    l[qt] = l_acc[qt][0];
     inv[qt] = l[qt] > 0.f ? 1.f / l[qt] : 0.f;
   }
   SA_LDS char* ob = buf + wave * 8192;
@@ -503,7 +511,7 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
     o[dt][1] = f32x4{};
   }
   float m_run[2] = {neg_inf(), neg_inf()};
-  float l_run[2] = {0.f, 0.f};
+  f32x4 l_acc[2] = {f32x4{}, f32x4{}};
   const float c = a.scale * kLog2e;
 
   // kernel arguments the tile loop needs, read once
@@ -527,7 +535,7 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
     // access), so that every tile issues the same copies and waits
     const __amdgpu_buffer_rsrc_t krs = make_rsrc((comp_next ? it.kdbase : it.kbase) + (int64_t)key0_next * kstride,
                                                  next ? (uint32_t)(klim_next - key0_next) * kstride : 0u);
-    d128_tile<CT>(lk, lv, L, qf, key0, klim, t < it.cnt ? 0.f : comp_bias, c, g, o, m_run, l_run,
+    d128_tile<CT>(lk, lv, L, qf, key0, klim, t < it.cnt ? 0.f : comp_bias, c, g, o, m_run, l_acc,
                   [&](int j) { d128_copy_one(lv, vrs, vstride, L.v_off, wave, j); },
                   [&](int j) { d128_copy_one(lk, krs, kstride, L.k_off, wave, j); });
     key0 = key0_next;
@@ -536,7 +544,7 @@ __global__ __launch_bounds__(256, 2) void block_sparse_fwd_d128_kernel(FwdArgs a
 
   // O through this wave's 8 KB of the K buffer: every wave has passed the last barrier, so
   // no wave still reads K and no copy into it is in flight.
-  d128_store_o_staged<CT>(a, it, o, m_run, l_run, lk, wave, lane);
+  d128_store_o_staged<CT>(a, it, o, m_run, l_acc, lk, wave, lane);
 }
 
 // fp32 operands: every value is split as x = hi + lo with hi = bf16(x) and

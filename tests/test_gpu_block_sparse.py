@@ -1,10 +1,12 @@
 """GPU parity of the block-sparse attention forward (sinkattn_block_sparse_fwd) against
 the fp32 dense masked-softmax oracle (oracle/torch_ref.dense_masked_attention).
 
-Tolerance (north star): max |out - ref| <= 2e-2 and mean |out - ref| <= 1e-3.  The lse
-the kernels write (fp32, the row sums taken in fp32 as the flash-attention forward does) is
-held to 1e-3 + 1e-5 |ref|; the drop-in's lse, cast to q.dtype like the reference's, to 2e-2
-plus that type's rounding.
+Tolerance (north star): max |out - ref| <= 2e-2 and mean |out - ref| <= 1e-3.  The fp32 lse
+the kernels write is held to 4e-3 + 1e-5 |ref|: the head-dim-128 kernel sums the 16-bit P
+values it multiplies V with (on the matrix cores), each within 2^-8 relative of the fp32
+value for bf16, so its row sum is within 2^-8 relative and its lse within log(1 + 2^-8) =
+3.9e-3 of the fp32 one (the other kernels sum fp32 P and stay near 1e-5).  The drop-in's lse,
+cast to q.dtype like the reference's, is held to 2e-2 plus that type's rounding.
 """
 import math
 
@@ -18,6 +20,7 @@ from sinkattn_amd import sparse_attention as sa
 pytestmark = pytest.mark.gpu
 
 MAX_ABS, MEAN_ABS = 2e-2, 1e-3
+LSE_ABS = 4e-3
 
 
 def _inputs(B, H, Nq, Nk, D, dtype, seed, sink_keys=0, sink_scale=8.0, layout="bhsd"):
@@ -61,7 +64,7 @@ def _check(out, lse, q, k, v, mask, rows=None, scale=None):
     fin = torch.isfinite(ref_l)
     assert torch.equal(fin, torch.isfinite(l))
     if lse.dtype == torch.float32:
-        assert ((l[fin] - ref_l[fin]).abs() <= 1e-3 + 1e-5 * ref_l[fin].abs()).all(), \
+        assert ((l[fin] - ref_l[fin]).abs() <= LSE_ABS + 1e-5 * ref_l[fin].abs()).all(), \
             (l[fin] - ref_l[fin]).abs().max().item()
     else:
         # lse from the drop-in API is cast to q.dtype like the reference's; allow that rounding

@@ -8,7 +8,7 @@ within one rounding of the dtype; the mix bit-exact with the reference's op sequ
 for bf16/f16 (one-ulp differences allowed on at most 1e-4 of the elements, for `exp`
 implementations that differ in the last fp32 bit), within 1e-5 relative for fp32; the fused
 attention 2e-2 max-abs / 1e-3 mean-abs against the fp32 union attention, its fp32 lse within
-1e-3 + 1e-5|lse|; against the reference's unfused sequence (whose LSEs
+4e-3 + 1e-5|lse| (row sums of the bf16 P values, log(1 + 2^-8) = 3.9e-3 at most); against the reference's unfused sequence (whose LSEs
 are rounded to bf16 before the mix) 2e-3 mean-abs and, per element, 2e-2 plus the
 largest shift that the reference's bf16 roundings of the LSEs and mix steps can cause."""
 import math
@@ -153,11 +153,10 @@ def test_fused_compensation_vs_oracle(N, gap, prefix, comp_rows, seed):
     err = (out.float().cpu() - want).abs()
     print(f"  vs fp32 union: max {err.max().item():.3e} mean {err.mean().item():.3e}", flush=True)
     assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
-    # the kernel's row sums add the bf16-rounded P values it multiplies V with (relative
-    # error <= 2^-9 per value), so the LSE is within 2^-8 of the fp32 one
+    # the kernel's row sums add the bf16 P values it multiplies V with (each within 2^-8
+    # relative of the fp32 value), so the lse is within log(1 + 2^-8) = 3.9e-3 of the fp32 one
     lerr = (lse.cpu() - want_lse).abs()
-    # fp32 lse with fp32 row sums: well inside 1e-3 (max 3e-6 at config 2 without compensation)
-    assert (lerr <= 1e-3 + 1e-5 * want_lse.abs()).all(), lerr.max().item()
+    assert (lerr <= 4e-3 + 1e-5 * want_lse.abs()).all(), lerr.max().item()
     # against the reference's unfused sequence (bf16 LSEs into the reference-rounded mix)
     so, sl = sa._block_sparse_attn(q, k, v, m.to(DEV), return_lse=True)
     full = torch.ones(B, H, -(-cr // 128), -(-kd.size(2) // 128), dtype=torch.bool, device=DEV)
