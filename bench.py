@@ -48,7 +48,7 @@ POOL_KERNEL_CYCLES = 1.173e7
 # 0.5 GiB for it -> x2.0, WRITE_SIZE reads 1 GiB -> x1.0).  Summaries with the commands:
 # profiles/block_sparse_fwd_wan_c2.md and profiles/block_mass_pool_wan_c2.md.
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
-TRAFFIC_KIB = {"fa": (1464336.0, 199631.0), "pool": (1278117.0, 792577.0)}
+TRAFFIC_KIB = {"fa": (1451332.0, 199631.0), "pool": (1279681.0, 792576.0)}
 
 
 def traffic_bytes(kind):

@@ -101,7 +101,9 @@ int sinkattn_block_sparse_plan_cached(const uint8_t* mask, const int64_t mask_st
  *     out = softmax(scale * Q K^T + M) V,   lse = log(sum(exp(scale * Q K^T + M)))
  * with M = 0 on listed tiles and -inf elsewhere.  q/k/v/out are BHSD-addressed (see
  * above), dtype one of sinkattn_dtype (f32 operands are rounded to bf16 for the matrix
- * cores; accumulation and softmax are fp32).  lse is fp32 [B,H,Nq] contiguous, or NULL.
+ * cores; accumulation and softmax are fp32).  lse is fp32 [B,H,Nq] contiguous, or NULL;
+ * for D = 128 with 16-bit operands the row sums add the 16-bit P values the PV product uses,
+ * so lse is within log(1 + 2^-8) of the exact value (bf16; 2^-11 for f16).
  * A row with no listed key block gets out = 0 and lse = +inf.
  * counts/idx/order come from sinkattn_block_sparse_plan (order may be NULL: one
  * work-group per row in row order).
