@@ -8,18 +8,18 @@
 // Work decomposition: one 256-thread work-group (4 waves) per (b, h, q-block); wave w
 // owns query rows [32w, 32w+32) of the block.  For every listed key block the group
 // brings K and V into LDS, then each wave runs
-//     S^T = K Q^T          v_mfma_f32_32x32x16 (A = K rows from LDS, B = Q^T in VGPRs)
+//     S^T = K Q^T          (A = K rows from LDS, B = Q^T in VGPRs)
 //     online softmax       exp2 domain, fp32
 //     O^T += V^T P^T       (A = V^T rows from LDS, B = P^T straight from the S^T VGPRs)
 // Computing the transposed products makes the S^T accumulator layout (one query column
 // per lane, keys down the registers) line up with the B-operand layout of the second
-// MFMA, so P never leaves registers.  The K rows fed as A operand are permuted (bits 2
-// and 3 of the row index swapped) so that the key order in the P^T registers is the
-// natural order.  block_sparse_fwd_kernel (D = 32 and 64) stages K and V^T through
-// registers, V transposed while staging; block_sparse_fwd_d128_kernel (D = 128, 16-bit)
-// copies K and V row-major by buffer DMA and reads V^T with transpose loads;
-// block_sparse_fwd_f32_kernel splits fp32 operands into bf16 pairs.  The plan kernels at
-// the end of the file turn the bool mask into per-row lists and the launch order.
+// MFMA, so P never leaves registers.  block_sparse_fwd_kernel (D = 32 and 64, all input
+// types; v_mfma_f32_32x32x16, K rows permuted so that the key order in the P^T registers is
+// natural) stages K and V^T through registers, V transposed while staging;
+// block_sparse_fwd_d128_kernel (D = 128, 16-bit; v_mfma_f32_16x16x32) copies K and V
+// row-major by buffer DMA and reads V^T with transpose loads; block_sparse_fwd_f32_kernel
+// splits fp32 operands into bf16 pairs.  The plan kernels at the end of the file turn the
+// bool mask into per-row lists and the launch order.
 
 #include "common.h"
 #include "kernels.h"
