@@ -4,14 +4,15 @@ with caller buffers, both through the C ABI.
 
 The two run the same kernels on the same plan, so the outputs must be bit-identical.  Two calls
 in a row, the second on a smaller input (the static array still holds the first call's larger
-plan), then the first shape again; plus the size limit, which is checked on the host before
-any launch."""
+plan), then the first shape again; the no-allocation path on its own against the oracle; plus
+the size limit, which is checked on the host before any launch."""
 import ctypes
 import math
 
 import pytest
 import torch
 
+from oracle import torch_ref
 from sinkattn_amd import _lib
 
 pytestmark = pytest.mark.gpu
@@ -89,6 +90,27 @@ def test_noalloc_matches_plan_and_forward_twice_then_smaller():
         assert _same(got_o, want_o)
         assert _same(got_l, want_l)
         assert torch.isinf(got_l[0, 0, (mask.shape[2] // 2) * 128]).item()   # the empty row
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_noalloc_against_the_oracle(dtype):
+    """The no-allocation path checked on its own against the oracle's dense masked softmax
+    (the same bars as the plan + forward parity tests: |dO| <= 2e-2 max and 1e-3 mean, fp32
+    lse within 4e-3 + 1e-5 |lse|, empty rows give out = 0 and lse = +inf), then once more on a
+    smaller shape after it, so the second call reads the plan the first one left behind."""
+    for B, H, N, seed, density in ((1, 3, 1300, 8, 0.35), (1, 2, 500, 9, 0.6)):
+        q, k, v, mask = _inputs(B, H, N, dtype, seed=seed, density=density)
+        print(f"noalloc vs oracle: {dtype} q {tuple(q.shape)} mask {tuple(mask.shape)}", flush=True)
+        out, lse = _noalloc(q, k, v, mask)
+        torch.cuda.synchronize()
+        ref_o, ref_l = torch_ref.dense_masked_attention(q, k, v, mask)
+        o, l = out.float().cpu(), lse.cpu()
+        err = (o - ref_o).abs()
+        assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3, (err.max().item(), err.mean().item())
+        fin = torch.isfinite(ref_l)
+        assert torch.equal(fin, torch.isfinite(l))
+        assert ((l[fin] - ref_l[fin]).abs() <= 4e-3 + 1e-5 * ref_l[fin].abs()).all()
+        assert torch.equal(o[~fin], torch.zeros_like(o[~fin]))
 
 
 def test_noalloc_f16_bshd_views():
